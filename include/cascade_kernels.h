@@ -1,0 +1,158 @@
+/*
+ * cascade_kernels.h - C ABI of the MI355X (gfx950) cascade-decode operator set.
+ *
+ * Every entry point takes raw device pointers, POD sizes/strides and a
+ * hipStream_t passed as `void *stream`, enqueues its kernels on that stream
+ * and returns without synchronising. Return value: 0 on success, a negative
+ * CK_E* code for a rejected argument (nothing is launched), or a positive
+ * hipError_t from the launch. Callers own every buffer, including the
+ * workspaces whose sizes the *_plan functions report. No entry point
+ * allocates or frees device memory.
+ *
+ * Reference interfaces replaced (paths relative to the reference root,
+ * ascend-kernel/csrc/ops/ abbreviated OPS/):
+ *   ck_lse_merge          <- device entry lse_merge(o1, o2, lse1, lse2, out,
+ *                            totalRows, dim, o1IsF32, outIsF32, lseStride1,
+ *                            lseStride2), OPS/lse_merge/op_kernel/kernel_lse_merge.cpp:343-346,
+ *                            launched from OPS/lse_merge/op_host/lse_merge.cpp:67-68
+ *   ck_fa_fp32_stage1     <- device entry fa_fp32_stage1(q, k, v, mask, blockTables, o,
+ *                            actualQseqlen, actualKvseqlen, s/p/oTemp/oUpdate workspaces,
+ *                            tiling, lse), OPS/fa_fp32_stage1/op_kernel/kernel_fa_fp32_stage1.cpp:848-863,
+ *                            launched from OPS/fa_fp32_stage1/op_host/fa_fp32_stage1.cpp:325-327
+ *   ck_suffix_decode      <- the stage-2 suffix attention the reference takes from the
+ *                            closed CANN op npu_fused_infer_attention_score_v2
+ *                            (call sites ascend-kernel/README.md:186-197,
+ *                            OPS/fa_fp32_stage1/test/run_merge_probe.py:173-179)
+ *   ck_f3_gateup_epilogue <- device entry f3_gateup_epilogue(a, b, workspace, d, m, nHalf,
+ *                            k, mode, dStride), OPS/f3_floor/op_kernel/kernel_f3_floor.cpp:319-321,
+ *                            launched from OPS/f3_floor/op_host/f3_floor.cpp:123
+ */
+#ifndef CASCADE_KERNELS_H
+#define CASCADE_KERNELS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error codes (negative; positive values are hipError_t) ---------------- */
+#define CK_OK 0
+#define CK_E_INVALID_ARG (-1)   /* a size, stride or mode is outside the supported domain */
+#define CK_E_NULL_PTR (-2)      /* a required pointer is NULL */
+#define CK_E_WORKSPACE (-3)     /* workspace missing or smaller than the plan requires */
+#define CK_E_UNSUPPORTED (-4)   /* shape supported by the API but not by a built kernel */
+
+/* Human-readable text for a code returned by any ck_* function. */
+const char *ck_error_string(int code);
+
+/* ---- element type tags ------------------------------------------------------ */
+#define CK_DTYPE_BF16 0
+#define CK_DTYPE_F32 1
+
+/* ============================================================================
+ * LSE merge of two partial attention results, per row r (fp32 arithmetic):
+ *   m = max(l1, l2); w1 = exp(l1 - m); w2 = exp(l2 - m); s = w1 + w2
+ *   out[r, :] = (o1[r, :] * w1 + o2[r, :] * w2) * (1 / s)
+ *   lse_out[r] = m + log(s)                         (when lse_out != NULL)
+ * One side at -inf contributes weight 0 (out equals the other side exactly).
+ * Both sides at -inf: out = 0 and lse_out = -inf.
+ *   o1, o2      [rows, dim], dtype o1_dtype / o2_dtype (CK_DTYPE_*)
+ *   lse1, lse2  fp32; row r's value is lse[r * lse_stride] (1 = compact,
+ *               8 = the padded layout ck_fa_fp32_stage1 writes)
+ *   out         [rows, dim], dtype out_dtype
+ *   lse_out     fp32 [rows] or NULL
+ * Domain: rows >= 0, dim > 0 and dim % 16 == 0, strides in [1, 64].
+ * Replaces OPS/lse_merge/op_kernel/kernel_lse_merge.cpp:343-346 (o2 fp32 and
+ * lse_out are additions; the reference takes o2 bf16 only and has no lse_out).
+ * ========================================================================== */
+int ck_lse_merge(const void *o1, int o1_dtype, const void *o2, int o2_dtype,
+                 const float *lse1, int64_t lse1_stride, const float *lse2, int64_t lse2_stride,
+                 void *out, int out_dtype, float *lse_out, int64_t rows, int64_t dim,
+                 void *stream);
+
+/* ============================================================================
+ * Stage-1 paged flash attention over a shared prefix (no mask, GQA).
+ *   q            bf16 [num_tokens, num_heads, 128]; request b owns tokens
+ *                [q_start(b), q_start(b) + q_len(b))
+ *   k, v         bf16 [num_blocks, 128, kv_heads, 128] (token-major pages)
+ *   block_table  int32 [batch, bt_cols]; logical kv token j of request b is
+ *                k[block_table[b * bt_cols + j / 128], j % 128, kv_head, :]
+ *   kv_seqlens   int64 [batch] on the device (read by the kernel)
+ *   q_seqlens    int64 [batch] on the device; read only when q_len_uniform == 0
+ *   q_start      int32 [batch] on the device; read only when q_len_uniform == 0
+ *   q_len_uniform  > 0: every request has this q length, q_start(b) = b * q_len_uniform
+ *                  = 0: per-request q_seqlens / q_start
+ *   max_q_len    upper bound of q_len(b) (equals q_len_uniform when that is > 0)
+ *   kv_cap       upper bound of kv_seqlens(b), <= bt_cols * 128; tokens beyond
+ *                min(kv_seqlens(b), bt_cols * 128) are never read
+ *   out          fp32 [num_tokens, num_heads, 128] = softmax(q k^T * scale) v
+ *   lse          fp32 [num_tokens * num_heads * 8]; row (t * num_heads + h)
+ *                holds 8 identical copies of log(sum exp(q k^T * scale))
+ *   workspace    device buffer of ck_fa_fp32_stage1_plan's workspace_bytes
+ *                (may be NULL when that is 0)
+ * P = exp(S - rowmax) is rounded to bf16 (RNE) before the PV product and the
+ * row sums use the unrounded fp32 values, as
+ * third_party/catlass/.../block_epilogue_online_softmax_no_mask.hpp:487-594 does.
+ * Replaces OPS/fa_fp32_stage1/op_kernel/kernel_fa_fp32_stage1.cpp:848-863.
+ * ========================================================================== */
+int ck_fa_fp32_stage1_plan(int64_t batch, int64_t max_q_len, int64_t num_heads, int64_t kv_heads,
+                           int64_t head_dim, int64_t kv_cap, int64_t *num_splits,
+                           int64_t *workspace_bytes);
+
+int ck_fa_fp32_stage1(const void *q, const void *k, const void *v, const int32_t *block_table,
+                      int64_t bt_cols, const int64_t *q_seqlens, const int64_t *kv_seqlens,
+                      const int32_t *q_start, int64_t batch, int64_t q_len_uniform,
+                      int64_t max_q_len, int64_t num_tokens, int64_t num_heads, int64_t kv_heads,
+                      int64_t head_dim, int64_t num_blocks, int64_t block_size, float scale,
+                      int64_t kv_cap, int64_t num_splits, float *out, float *lse,
+                      void *workspace, int64_t workspace_bytes, void *stream);
+
+/* ============================================================================
+ * Per-sequence paged decode attention over each sequence's own suffix
+ * (one query token per sequence, GQA, no MFMA).
+ *   q            bf16 [batch, num_heads, 128]
+ *   k, v         bf16 [num_blocks, 128, kv_heads, 128]
+ *   block_table  int32 [batch, bt_cols]; kv_seqlens int64 [batch] on the device
+ *   out          bf16 [batch, num_heads, 128]
+ *   lse          fp32 [batch * num_heads] (compact); a sequence with kv length 0
+ *                gets out = 0 and lse = -inf (an empty suffix)
+ *   kv_cap       upper bound of kv_seqlens(b), <= bt_cols * 128
+ * Same softmax arithmetic as ck_fa_fp32_stage1 (fp32 accumulation).
+ * Replaces the closed CANN op npu_fused_infer_attention_score_v2 used as
+ * stage 2 (ascend-kernel/README.md:186-197).
+ * ========================================================================== */
+int ck_suffix_decode_plan(int64_t batch, int64_t num_heads, int64_t kv_heads, int64_t head_dim,
+                          int64_t kv_cap, int64_t *num_splits, int64_t *workspace_bytes);
+
+int ck_suffix_decode(const void *q, const void *k, const void *v, const int32_t *block_table,
+                     int64_t bt_cols, const int64_t *kv_seqlens, int64_t batch, int64_t num_heads,
+                     int64_t kv_heads, int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                     float scale, int64_t kv_cap, int64_t num_splits, void *out, float *lse,
+                     void *workspace, int64_t workspace_bytes, void *stream);
+
+/* ============================================================================
+ * gate_up GEMM with the epilogue ladder of OPS/f3_floor (bf16, fp32 accumulate).
+ *   a          bf16 [m, k] row-major (activations)
+ *   b          bf16 [2 * n_half, k] row-major (nn.Linear weight: gate rows
+ *              0..n_half-1, up rows n_half..2*n_half-1)
+ *   workspace  bf16 [m, 2 * n_half] = C = a b^T (RNE), written by modes
+ *              0, 2, 4, 5, 7, 8; read by mode 3; untouched by mode 1
+ *   d          bf16 [m, n_half] with row stride d_stride (elements)
+ *   mode 0: d = C[:, :n_half]            mode 1: d = silu(g) * u, fused: g and u
+ *   mode 2: C only                                are the fp32 accumulators
+ *   mode 3: d = workspace[:, :n_half]    mode 4: d = C[:, n_half:]
+ *   mode 5: d = C[:, :n_half]            mode 7: C only (d not written)
+ *   mode 8: C, and d = 0
+ * Domain: m >= 1, k >= 64 and k % 16 == 0, n_half % 128 == 0,
+ * d_stride >= n_half. silu(x) = x / (1 + exp(-x)).
+ * Replaces OPS/f3_floor/op_kernel/kernel_f3_floor.cpp:319-321.
+ * ========================================================================== */
+int ck_f3_gateup_epilogue(const void *a, const void *b, void *workspace, void *d, int64_t m,
+                          int64_t n_half, int64_t k, int64_t mode, int64_t d_stride, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CASCADE_KERNELS_H */

@@ -1,0 +1,29 @@
+"""Test configuration: import paths and the ``gpu`` marker.
+
+``-m "not gpu"``: the oracle against the reference's fixtures and mathematics,
+host-side validation (meta tensors), and that the C-ABI library loads and
+exports every symbol of include/cascade_kernels.h.
+``-m gpu``: parity of the HIP kernels (through the C ABI and the torch ops)
+against the oracle on seeded inputs.
+"""
+import os
+import sys
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(REPO, "vllm-hust-cascade-kernel_amd")
+for p in (REPO, PKG):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+GOLDEN = os.path.join(REPO, "tests", "golden")
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+
+
+@pytest.fixture(scope="session")
+def golden_dir():
+    return GOLDEN

@@ -1,0 +1,73 @@
+"""CPU checks of the C-ABI library: it loads without a GPU, exports every symbol
+include/cascade_kernels.h declares, and rejects bad arguments before any launch."""
+import ctypes
+
+import pytest
+
+from cascade_amd import abi
+
+
+def test_library_exports_every_header_symbol():
+    names = abi.header_symbols()
+    assert names == sorted(abi.SIGNATURES), (names, sorted(abi.SIGNATURES))
+    handle = ctypes.CDLL(abi.KERNEL_LIB)
+    for n in names:
+        assert hasattr(handle, n), n
+
+
+def test_error_strings():
+    assert abi.error_string(0) == "success"
+    for code in (-1, -2, -3, -4):
+        assert abi.error_string(code) and abi.error_string(code) != "unknown error"
+
+
+def test_merge_argument_validation_without_launch():
+    L = abi.lib()
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation first
+    assert L.ck_lse_merge(p, 0, p, 0, p, 1, p, 1, p, 0, None, 4, 15, None) == -1   # dim % 16
+    assert L.ck_lse_merge(p, 0, p, 0, p, 65, p, 1, p, 0, None, 4, 16, None) == -1  # stride > 64
+    assert L.ck_lse_merge(p, 2, p, 0, p, 1, p, 1, p, 0, None, 4, 16, None) == -1   # dtype tag
+    assert L.ck_lse_merge(None, 0, p, 0, p, 1, p, 1, p, 0, None, 4, 16, None) == -2
+    assert L.ck_lse_merge(None, 0, None, 0, None, 1, None, 1, None, 0, None, 0, 16, None) == 0  # empty
+
+
+def test_stage1_plan_and_validation():
+    s, w = abi.stage1_plan(1, 64, 32, 8, 128, 8192)        # config 2, flattened
+    assert s > 1 and w == s * 64 * 32 * 129 * 4
+    s, w = abi.stage1_plan(64, 1, 32, 8, 128, 8192)        # per-request decode: no split
+    assert s == 1 and w == 0
+    s, w = abi.stage1_plan(1, 256, 64, 8, 128, 32768)      # config 5 prefix
+    assert s >= 1
+    out = ctypes.c_int64(0)
+    L = abi.lib()
+    assert L.ck_fa_fp32_stage1_plan(1, 1, 30, 8, 128, 100, ctypes.byref(out), ctypes.byref(out)) == -1  # H % KVH
+    assert L.ck_fa_fp32_stage1_plan(1, 1, 32, 8, 64, 100, ctypes.byref(out), ctypes.byref(out)) == -4   # D != 128
+    p = ctypes.c_void_p(16)
+    # block size 64 unsupported; kv_cap beyond the table: both refused before launch
+    assert L.ck_fa_fp32_stage1(p, p, p, p, 1, p, p, None, 1, 1, 1, 1, 8, 8, 128, 1, 64, 0.1, 128, 1, p, p,
+                               None, 0, None) == -4
+    assert L.ck_fa_fp32_stage1(p, p, p, p, 1, p, p, None, 1, 1, 1, 1, 8, 8, 128, 1, 128, 0.1, 256, 1, p, p,
+                               None, 0, None) == -1
+    # a split plan without a workspace
+    assert L.ck_fa_fp32_stage1(p, p, p, p, 64, p, p, None, 1, 64, 64, 64, 32, 8, 128, 64, 128, 0.1, 8192, 0,
+                               p, p, None, 0, None) == -3
+
+
+def test_suffix_plan_and_validation():
+    s, w = abi.suffix_plan(64, 32, 8, 128, 4096)
+    assert s >= 1 and (w == 0) == (s == 1)
+    L = abi.lib()
+    out = ctypes.c_int64(0)
+    assert L.ck_suffix_decode_plan(4, 64, 4, 128, 100, ctypes.byref(out), ctypes.byref(out)) == -4  # group 16
+    p = ctypes.c_void_p(16)
+    assert L.ck_suffix_decode(p, p, p, p, 1, p, 0, 8, 8, 128, 1, 128, 0.1, 128, 1, p, p, None, 0, None) == 0
+
+
+def test_gemm_validation():
+    L = abi.lib()
+    p = ctypes.c_void_p(16)
+    assert L.ck_f3_gateup_epilogue(p, p, p, p, 16, 100, 128, 1, 100, None) == -1  # I % 128
+    assert L.ck_f3_gateup_epilogue(p, p, p, p, 16, 128, 72, 1, 128, None) == -1   # K % 16
+    assert L.ck_f3_gateup_epilogue(p, p, p, p, 16, 128, 128, 6, 128, None) == -1  # mode 6
+    assert L.ck_f3_gateup_epilogue(p, p, None, p, 16, 128, 128, 0, 128, None) == -2  # mode 0 needs C
+    assert L.ck_f3_gateup_epilogue(p, p, p, p, 0, 128, 128, 1, 128, None) == -1   # M = 0

@@ -1,0 +1,248 @@
+"""GPU parity of fa_fp32_stage1 against the oracle (fa_fp32_ref restatement) and
+dense attention, following the reference's suites (run_precision_suite.py,
+test_q_seqlen_fastpath.py, test_lse_flatten_regression.py) with permuted block
+tables added.
+
+Tolerances (north star): O max-abs 2e-3, LSE 1e-4 relative. The kernel rounds P
+to bf16 at its own tile boundaries, so O is also held to the bf16-P bound
+|O - O_dense| <= 2^-8 * max|v| + 1e-5 against exact softmax attention.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle.bf16 import bits_to_f32, bf16_bits
+from oracle.inputs import paged_inputs
+from tests._util import torch_bf16
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _lib():
+    import cascade_amd  # noqa: F401
+    if not torch.cuda.is_available():
+        pytest.fail("no GPU visible to torch")
+
+
+def _dev(inp):
+    return (torch_bf16(inp["q16"], DEV), torch_bf16(inp["k16"], DEV), torch_bf16(inp["v16"], DEV),
+            torch.from_numpy(inp["block_table"]).to(DEV), torch.from_numpy(inp["q_seqlens"]).to(DEV),
+            torch.from_numpy(inp["kv_seqlens"]).to(DEV))
+
+
+def _run(inp, q_seqlen_value=0):
+    args = _dev(inp)
+    out, lse = torch.ops.npu.fa_fp32_stage1(*args, q_seqlen_value)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), lse.cpu().numpy()
+
+
+def _check(inp, out, lse, H):
+    T = inp["num_tokens"]
+    assert out.shape == (T, H, 128) and lse.shape == (T * H * 8,)
+    L, same = A.unpack_lse(lse, T, H)
+    assert same, "the 8 LSE copies of a row differ"
+    O_ref, L_ref = A.stage1(inp["q"], inp["k"], inp["v"], inp["block_table"], inp["q_seqlens"],
+                            inp["kv_seqlens"])
+    O_dense, _ = A.stage1(inp["q"], inp["k"], inp["v"], inp["block_table"], inp["q_seqlens"],
+                          inp["kv_seqlens"], chunk=None, quantize_p=False)
+    o_err = np.abs(out.astype(np.float64) - O_ref).max()
+    l_rel = (np.abs(L.astype(np.float64) - L_ref) / np.maximum(np.abs(L_ref), 1.0)).max()
+    d_err = np.abs(out.astype(np.float64) - O_dense).max()
+    vmax = float(np.abs(inp["v"]).max())
+    assert o_err <= 2e-3, o_err
+    assert l_rel <= 1e-4, l_rel
+    assert d_err <= 2.0 ** -8 * vmax + 1e-5, d_err
+    return o_err, l_rel
+
+
+# (name, batch, kv_seqlens, H, KVH, q_len, cols_extra): run_precision_suite.py:19-36, sizes trimmed
+CASES = [
+    ("probe_shape_b4", 4, [4096] * 4, 40, 8, 1, 0),
+    ("b16_h32", 16, [2048] * 16, 32, 8, 1, 0),
+    ("b8_h8_kvh1", 8, [2048] * 8, 8, 1, 1, 0),
+    ("min_b1_kv128", 1, [128], 40, 8, 1, 0),
+    ("kv_448_tail", 3, [448] * 3, 40, 8, 1, 0),
+    ("varlen_3req", 3, [129, 640, 1024], 40, 8, 1, 0),
+    ("qlen2_b4", 4, [2048] * 4, 40, 8, 2, 0),
+    ("b64_kv128", 64, [128] * 64, 40, 8, 1, 0),
+    ("h2_kvh1", 4, [512] * 4, 2, 1, 1, 0),
+    ("padded_block_cols", 4, [4096] * 4, 40, 8, 1, 3),
+    ("varlen_6req", 6, [4095, 2048, 8192, 512, 128, 4096], 40, 8, 1, 0),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+@pytest.mark.parametrize("share", [True, False], ids=["shared", "distinct"])
+def test_precision_suite(case, share):
+    name, batch, kvs, H, KVH, q_len, extra = case
+    cols = None if extra == 0 else max((kv + 127) // 128 for kv in kvs) + extra
+    inp = paged_inputs(batch, kvs, H, KVH, seed=len(name), q_len=q_len, block_cols=cols, share_blocks=share,
+                       permute=True)
+    out_d, lse_d = _run(inp, 0)
+    _check(inp, out_d, lse_d, H)
+    # fast path (q_seqlen_value = q_len) is bit-identical to the default path
+    out_f, lse_f = _run(inp, q_len)
+    assert np.array_equal(out_d.view(np.uint32), out_f.view(np.uint32))
+    assert np.array_equal(lse_d.view(np.uint32), lse_f.view(np.uint32))
+
+
+# test_lse_flatten_regression.py:30-47: B=1 flattened form, q_len = T
+FLAT = [("flat_T64_kv128", 64, 40, 8, 128), ("flat_T64_kv4356", 64, 40, 8, 4356),
+        ("flat_T8_3b", 8, 16, 2, 4096), ("flat_T17_bnd", 17, 40, 8, 4096), ("flat_T63_odd", 63, 40, 8, 4096)]
+
+
+@pytest.mark.parametrize("case", FLAT, ids=[c[0] for c in FLAT])
+def test_flattened_form(case):
+    name, T, H, KVH, kv = case
+    inp = paged_inputs(1, [kv], H, KVH, seed=3, q_len=T, permute=True)
+    out, lse = _run(inp, T)
+    _check(inp, out, lse, H)
+
+
+def test_varlen_q_default_path():
+    """Per-request q lengths differ (default path pulls seqlens to the host)."""
+    inp = paged_inputs(3, [300, 1000, 70], 16, 4, seed=9, q_len=1, permute=True)
+    rng = np.random.default_rng(0)
+    qlens = np.array([5, 1, 40], dtype=np.int64)
+    T = int(qlens.sum())
+    q = rng.standard_normal((T, 16, 128)).astype(np.float32)
+    inp["q16"] = bf16_bits(q)
+    inp["q"] = bits_to_f32(inp["q16"])
+    inp["q_seqlens"] = qlens
+    inp["num_tokens"] = T
+    out, lse = _run(inp, 0)
+    _check(inp, out, lse, 16)
+
+
+def test_config2_llama8b_flattened_and_per_request():
+    """H=32, KVH=8, shared 8192-token prefix in permuted pages,
+    64 decode queries. Flattened call (bt [1,64], q_seqlen_value=64) and the
+    per-request form (bt [64,64], q_seqlen_value=1) agree within tolerance."""
+    B, H, KVH, P = 64, 32, 8, 8192
+    inp = paged_inputs(1, [P], H, KVH, seed=0, q_len=B, permute=True)
+    out, lse = _run(inp, B)
+    _check(inp, out, lse, H)
+    per = dict(inp)
+    per["block_table"] = np.repeat(inp["block_table"], B, axis=0)
+    per["q_seqlens"] = np.ones(B, dtype=np.int64)
+    per["kv_seqlens"] = np.full(B, P, dtype=np.int64)
+    out2, lse2 = _run(per, 1)
+    assert np.abs(out2 - out).max() <= 2e-3
+    L1, _ = A.unpack_lse(lse, B, H)
+    L2, _ = A.unpack_lse(lse2, B, H)
+    assert np.abs(L1 - L2).max() <= 1e-4 * np.abs(L1).max()
+
+
+def test_block_table_indexing_bit_exact():
+    """One-hot attention through a permuted table: every query row selects a single
+    kv token (score 362 vs 0), so O equals that token's V row exactly; V rows encode
+    (page, row, kv head) as small integers (exact in bf16)."""
+    rng = np.random.default_rng(5)
+    B, H, KVH, D, kv = 3, 8, 2, 128, 700
+    inp = paged_inputs(B, [kv] * B, H, KVH, seed=5, permute=True, q_len=2)
+    nb = inp["k16"].shape[0]
+    k = np.zeros((nb, 128, KVH, D), dtype=np.float32)
+    v = np.zeros((nb, 128, KVH, D), dtype=np.float32)
+    v[:, :, :, 0] = np.arange(nb)[:, None, None]
+    v[:, :, :, 1] = np.arange(128)[None, :, None]
+    v[:, :, :, 2] = np.arange(KVH)[None, None, :]
+    q = np.zeros((B * 2, H, D), dtype=np.float32)
+    expect = np.zeros((B * 2, H, 3))
+    bt = inp["block_table"]
+    for b in range(B):
+        for g in range(KVH):
+            toks = rng.choice(kv, size=D, replace=False)
+            for dct, j in enumerate(toks):
+                k[bt[b, j // 128], j % 128, g, dct] = 64.0
+            for t in range(2):
+                for hq in range(H // KVH):
+                    h = g * (H // KVH) + hq
+                    sel = rng.integers(D)
+                    q[b * 2 + t, h, sel] = 64.0
+                    j = toks[sel]
+                    expect[b * 2 + t, h] = (bt[b, j // 128], j % 128, g)
+    inp.update(q16=bf16_bits(q), k16=bf16_bits(k), v16=bf16_bits(v))
+    out, _ = _run(inp, 2)
+    assert np.array_equal(out[:, :, :3], expect)
+    assert np.all(out[:, :, 3:] == 0)
+
+
+def test_catlass_fixture(golden_dir):
+    """The reference's example-23 inputs (q.bin, contiguous block_table [4,32],
+    kv 4096 x 4, H=40, KVH=8) with synthetic U(-1,1) K/V: parity with the oracle,
+    and the golden LSE statistics hold for the kernel too."""
+    d = os.path.join(golden_dir, "catlass_example")
+    q16 = np.fromfile(os.path.join(d, "q.bin"), dtype=np.uint16).reshape(4, 40, 128)
+    bt = np.fromfile(os.path.join(d, "block_table.bin"), dtype=np.int32).reshape(4, 32)
+    kvs = np.fromfile(os.path.join(d, "kv_seqlen.bin"), dtype=np.int64)
+    qs = np.fromfile(os.path.join(d, "q_seqlen.bin"), dtype=np.int64)
+    lse_g = np.fromfile(os.path.join(d, "golden_gpu_lse.bin"), dtype=np.float32)
+    rng = np.random.default_rng(0)
+    k16 = bf16_bits(rng.uniform(-1, 1, (128, 128, 8, 128)))
+    v16 = bf16_bits(rng.uniform(-1, 1, (128, 128, 8, 128)))
+    inp = dict(q16=q16, k16=k16, v16=v16, q=bits_to_f32(q16), k=bits_to_f32(k16), v=bits_to_f32(v16),
+               block_table=bt, q_seqlens=qs, kv_seqlens=kvs, num_tokens=4)
+    out, lse = _run(inp, 0)
+    _check(inp, out, lse, 40)
+    L, _ = A.unpack_lse(lse, 4, 40)
+    assert abs(L.mean() - lse_g.mean()) < 3e-3
+
+
+def test_stability_10_runs():
+    inp = paged_inputs(1, [8192], 40, 8, seed=3, q_len=64, permute=True)
+    args = _dev(inp)
+    first = None
+    for _ in range(10):
+        o, l = torch.ops.npu.fa_fp32_stage1(*args, 64)
+        b = (o.cpu().numpy().tobytes(), l.cpu().numpy().tobytes())
+        first = first or b
+        assert b == first
+
+
+def test_abi_direct_matches_torch_op():
+    from cascade_amd import abi
+    inp = paged_inputs(2, [1000, 333], 16, 4, seed=4, q_len=3, permute=True)
+    q, k, v, bt, qs, kvs = _dev(inp)
+    T, H = inp["num_tokens"], 16
+    splits, ws_bytes = abi.stage1_plan(2, 3, H, 4, 128, bt.shape[1] * 128)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+    out = torch.empty(T, H, 128, dtype=torch.float32, device=DEV)
+    lse = torch.empty(T * H * 8, dtype=torch.float32, device=DEV)
+    rc = abi.lib().ck_fa_fp32_stage1(q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), bt.shape[1],
+                                     qs.data_ptr(), kvs.data_ptr(), None, 2, 3, 3, T, H, 4, 128, k.shape[0], 128,
+                                     float(np.float32(1 / np.sqrt(128))), bt.shape[1] * 128, splits,
+                                     out.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws_bytes,
+                                     torch.cuda.current_stream().cuda_stream)
+    abi.check(rc)
+    o2, l2 = torch.ops.npu.fa_fp32_stage1(q, k, v, bt, qs, kvs, 3)
+    assert torch.equal(out, o2) and torch.equal(lse, l2)
+    # an undersized workspace is refused before any launch
+    if ws_bytes > 0:
+        assert abi.lib().ck_fa_fp32_stage1(q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), bt.shape[1],
+                                           qs.data_ptr(), kvs.data_ptr(), None, 2, 3, 3, T, H, 4, 128,
+                                           k.shape[0], 128, 0.088, bt.shape[1] * 128, splits, out.data_ptr(),
+                                           lse.data_ptr(), ws.data_ptr(), ws_bytes - 1,
+                                           torch.cuda.current_stream().cuda_stream) == -3
+
+
+def test_negative_checks():
+    inp = paged_inputs(4, [4096] * 4, 40, 8, seed=0, share_blocks=True)
+    q, k, v, bt, qs, kvs = _dev(inp)
+    with pytest.raises(RuntimeError, match="fa_fp32_stage1"):
+        torch.ops.npu.fa_fp32_stage1(q[:-1], k, v, bt, qs, kvs)            # T mismatch
+    with pytest.raises(RuntimeError, match="fa_fp32_stage1"):
+        torch.ops.npu.fa_fp32_stage1(q, k, v, bt[:, :1].contiguous(), qs, kvs)  # cols too small
+    bad_kv = kvs.clone()
+    bad_kv[3] = 0
+    with pytest.raises(RuntimeError, match="fa_fp32_stage1"):
+        torch.ops.npu.fa_fp32_stage1(q, k, v, bt, qs, bad_kv)               # kv seqlen 0
+    with pytest.raises(RuntimeError, match="q_seqlen_value"):
+        torch.ops.npu.fa_fp32_stage1(q, k, v, bt, qs, kvs, 2)               # T != 2B
+    o, l = torch.ops.npu.fa_fp32_stage1(q[:0], k, v, bt, qs[:0], kvs[:0])
+    assert o.shape == (0, 40, 128) and l.shape == (0,)

@@ -1,0 +1,154 @@
+"""GPU parity of suffix_decode (stage 2) and of the full cascade (stage 1 + suffix
++ merge) against the oracle and dense attention over the concatenated KV.
+
+suffix_decode keeps P in fp32, so its oracle is the unquantised online softmax.
+Its O is bf16: the tolerance is the north-star 2e-3 plus half a bf16 ulp of |O|.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle.bf16 import bits_to_f32, bf16_bits
+from oracle.inputs import paged_inputs
+from oracle.merge import merge_fp64
+from tests._util import bf16_to_np, torch_bf16
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _lib():
+    import cascade_amd  # noqa: F401
+    if not torch.cuda.is_available():
+        pytest.fail("no GPU visible to torch")
+
+
+def _suffix(inp):
+    q = torch_bf16(inp["q16"], DEV)
+    k = torch_bf16(inp["k16"], DEV)
+    v = torch_bf16(inp["v16"], DEV)
+    bt = torch.from_numpy(inp["block_table"]).to(DEV)
+    kvs = torch.from_numpy(inp["kv_seqlens"]).to(DEV)
+    out, lse = torch.ops.npu.suffix_decode(q, k, v, bt, kvs)
+    torch.cuda.synchronize()
+    return bf16_to_np(out), lse.cpu().numpy()
+
+
+def _check_suffix(inp, out, lse, H):
+    B = inp["q"].shape[0]
+    O_ref, L_ref = A.stage1(inp["q"], inp["k"], inp["v"], inp["block_table"], np.ones(B, dtype=np.int64),
+                            inp["kv_seqlens"], quantize_p=False)
+    L = lse.reshape(B, H)
+    err = np.abs(out - O_ref)
+    assert np.all(err <= 2e-3 + 2.0 ** -8 * np.abs(O_ref)), err.max()
+    fin = np.isfinite(L_ref)
+    assert np.array_equal(np.isfinite(L), fin)
+    assert np.all(np.isneginf(L[~fin]))
+    assert np.all(out[~fin] == 0)
+    if fin.any():
+        rel = np.abs(L[fin] - L_ref[fin]) / np.maximum(np.abs(L_ref[fin]), 1.0)
+        assert rel.max() <= 1e-4, rel.max()
+
+
+SUFFIX_CASES = [
+    ("decode_b8_h32", 8, [1, 2, 63, 64, 65, 127, 128, 300], 32, 8),
+    ("empty_and_short", 6, [0, 1, 0, 17, 200, 0], 16, 4),
+    ("long_multi_split", 3, [3000, 4096, 513], 32, 8),
+    ("gqa8_h64", 5, [700, 90, 1025, 2, 4000], 64, 8),
+    ("mha_h8_kvh8", 4, [100, 200, 300, 400], 8, 8),
+    ("group2", 4, [257, 33, 1000, 5], 8, 4),
+]
+
+
+@pytest.mark.parametrize("case", SUFFIX_CASES, ids=[c[0] for c in SUFFIX_CASES])
+def test_suffix_cases(case):
+    name, B, kvs, H, KVH = case
+    inp = paged_inputs(B, kvs, H, KVH, seed=len(name), permute=True)
+    out, lse = _suffix(inp)
+    _check_suffix(inp, out, lse, H)
+
+
+def test_suffix_geometric_lengths():
+    """BASELINE config 5's suffix distribution (geometric, mean 512, clipped to
+    [1, 4096]) at a reduced batch."""
+    rng = np.random.default_rng(1)
+    B, H, KVH = 24, 64, 8
+    kvs = np.clip(rng.geometric(1 / 512, size=B), 1, 4096)
+    inp = paged_inputs(B, kvs, H, KVH, seed=2, permute=True, block_cols=32)
+    out, lse = _suffix(inp)
+    _check_suffix(inp, out, lse, H)
+
+
+def test_suffix_abi_matches_torch_op():
+    from cascade_amd import abi
+    inp = paged_inputs(4, [1500, 10, 0, 900], 32, 8, seed=3, permute=True)
+    q = torch_bf16(inp["q16"], DEV)
+    k = torch_bf16(inp["k16"], DEV)
+    v = torch_bf16(inp["v16"], DEV)
+    bt = torch.from_numpy(inp["block_table"]).to(DEV)
+    kvs = torch.from_numpy(inp["kv_seqlens"]).to(DEV)
+    cap = bt.shape[1] * 128
+    s, wsb = abi.suffix_plan(4, 32, 8, 128, cap)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    out = torch.empty(4, 32, 128, dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty(4 * 32, dtype=torch.float32, device=DEV)
+    rc = abi.lib().ck_suffix_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), bt.shape[1],
+                                    kvs.data_ptr(), 4, 32, 8, 128, k.shape[0], 128,
+                                    float(np.float32(1 / np.sqrt(128))), cap, s, out.data_ptr(), lse.data_ptr(),
+                                    ws.data_ptr(), wsb, torch.cuda.current_stream().cuda_stream)
+    abi.check(rc)
+    o2, l2 = torch.ops.npu.suffix_decode(q, k, v, bt, kvs)
+    assert torch.equal(out, o2) and torch.equal(lse, l2)
+
+
+def _cascade_inputs(B, H, KVH, P, suf, seed):
+    rng = np.random.default_rng(seed)
+    nsb = [(int(s) + 127) // 128 for s in suf]
+    nblocks = P // 128 + sum(nsb)
+    k = rng.standard_normal((nblocks, 128, KVH, 128)).astype(np.float32)
+    v = rng.standard_normal((nblocks, 128, KVH, 128)).astype(np.float32)
+    q = rng.standard_normal((B, H, 128)).astype(np.float32)
+    perm = rng.permutation(nblocks).astype(np.int32)
+    bt_pre = perm[:P // 128][None, :].copy()
+    bt_suf = np.zeros((B, max(max(nsb), 1)), dtype=np.int32)
+    off = P // 128
+    for b in range(B):
+        bt_suf[b, :nsb[b]] = perm[off:off + nsb[b]]
+        off += nsb[b]
+    return bf16_bits(q), bf16_bits(k), bf16_bits(v), bt_pre, bt_suf, np.asarray(suf, dtype=np.int64)
+
+
+@pytest.mark.parametrize("cfg", [(8, 8, 2, 1024, "u64_256"), (16, 32, 8, 2048, "geo512"), (4, 32, 8, 512, "with_empty")],
+                         ids=["config1_b8_h8", "b16_h32_geo", "empty_suffix"])
+def test_cascade_equals_dense_over_concat(cfg):
+    """Config 1 shape (and two more): cascade_decode == softmax attention over the
+    concatenated prefix + suffix KV (bf16 output)."""
+    import cascade_amd
+    B, H, KVH, P, dist = cfg
+    rng = np.random.default_rng(B)
+    if dist == "u64_256":
+        suf = rng.integers(64, 257, size=B)
+    elif dist == "geo512":
+        suf = np.clip(rng.geometric(1 / 512, size=B), 1, 4096)
+    else:
+        suf = np.array([0, 5, 0, 300])
+    q16, k16, v16, bt_pre, bt_suf, suf = _cascade_inputs(B, H, KVH, P, suf, seed=B)
+    q, k, v = (torch_bf16(x, DEV) for x in (q16, k16, v16))
+    out = cascade_amd.ops.cascade_decode(q, k, v, torch.from_numpy(bt_pre).to(DEV), P, k, v,
+                                         torch.from_numpy(bt_suf).to(DEV), torch.from_numpy(suf).to(DEV))
+    got = bf16_to_np(out)
+    qf, kf, vf = bits_to_f32(q16), bits_to_f32(k16), bits_to_f32(v16)
+    for b in range(B):
+        kp, vp = A.gather_kv(kf, vf, bt_pre[0], P)
+        ks, vs = A.gather_kv(kf, vf, bt_suf[b], int(suf[b]))
+        Od, _ = A.dense(qf[b:b + 1], A.expand_heads(np.concatenate([kp, ks]), H),
+                        A.expand_heads(np.concatenate([vp, vs]), H))
+        err = np.abs(got[b:b + 1] - Od)
+        assert np.all(err <= 2e-3 + 2.0 ** -8 * np.abs(Od)), (b, err.max())
+    # and equals the oracle's own cascade composition
+    O1, L1 = A.stage1(qf, kf, vf, bt_pre, [B], [P])
+    O2, L2 = A.stage1(qf, kf, vf, bt_suf, np.ones(B, dtype=np.int64), suf, quantize_p=False)
+    Om, _ = merge_fp64(O1, O2, L1, L2)
+    assert np.all(np.abs(got - Om) <= 2e-3 + 2.0 ** -8 * np.abs(Om))

@@ -1,0 +1,51 @@
+"""Python-facing wrappers over ``torch.ops.npu.*`` (names follow the reference).
+
+``cascade_decode`` is the caller-side composition the reference documents
+(ascend-kernel/README.md:160-201): stage-1 over the shared prefix in the
+flattened form (one request, q_len = batch, ``q_seqlen_value = batch``), the
+per-sequence suffix attention, and the LSE merge of the two partial results.
+"""
+import torch
+
+
+def fa_fp32_stage1(query, key, value, block_table, actual_q_seqlens, actual_kv_seqlens, q_seqlen_value=0):
+    return torch.ops.npu.fa_fp32_stage1(query, key, value, block_table, actual_q_seqlens,
+                                        actual_kv_seqlens, q_seqlen_value)
+
+
+def lse_merge(o1, o2, lse1, lse2, out_code=0):
+    return torch.ops.npu.lse_merge(o1, o2, lse1, lse2, out_code)
+
+
+def lse_merge_with_lse(o1, o2, lse1, lse2, out_code=0):
+    return torch.ops.npu.lse_merge_with_lse(o1, o2, lse1, lse2, out_code)
+
+
+def suffix_decode(query, key, value, block_table, actual_kv_seqlens):
+    return torch.ops.npu.suffix_decode(query, key, value, block_table, actual_kv_seqlens)
+
+
+def f3_gateup_epilogue(a, b, workspace=None, out_d=None, mode=1):
+    return torch.ops.npu.f3_gateup_epilogue(a, b, workspace, out_d, mode)
+
+
+def swiglu_gate_up(a, b):
+    """D = silu(a @ b[:I].T) * (a @ b[I:].T) in one fused GEMM (mode 1)."""
+    return torch.ops.npu.f3_gateup_epilogue(a, b, None, None, 1)[0]
+
+
+def cascade_decode(query, prefix_key, prefix_value, prefix_block_table, prefix_len,
+                   suffix_key, suffix_value, suffix_block_table, suffix_kv_seqlens, out_code=1):
+    """Shared-prefix cascade decode for a batch of B single-token queries.
+
+    query [B,H,D] bf16; prefix pages shared by all B sequences (prefix_block_table
+    [1, cols]); each sequence's suffix through its own suffix_block_table row.
+    Returns the merged attention output [B,H,D] (bf16 for out_code=1).
+    """
+    B = query.shape[0]
+    dev = query.device
+    qlens = torch.tensor([B], dtype=torch.int64, device=dev)
+    kvlens = torch.tensor([prefix_len], dtype=torch.int64, device=dev)
+    o1, l1 = torch.ops.npu.fa_fp32_stage1(query, prefix_key, prefix_value, prefix_block_table, qlens, kvlens, B)
+    o2, l2 = torch.ops.npu.suffix_decode(query, suffix_key, suffix_value, suffix_block_table, suffix_kv_seqlens)
+    return torch.ops.npu.lse_merge(o1, o2, l1, l2, out_code)

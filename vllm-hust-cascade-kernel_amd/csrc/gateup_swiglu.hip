@@ -1,0 +1,262 @@
+// gateup_swiglu.hip - gate_up GEMM with the f3 epilogue ladder on gfx950 MFMA.
+//
+// Semantics (reference: ascend-kernel/csrc/ops/f3_floor, kernel
+// op_kernel/kernel_f3_floor.cpp:137-349, host op_host/f3_floor.cpp:59-124):
+//   a [M, K] bf16 activations, b [2I, K] bf16 nn.Linear weight (gate rows
+//   0..I-1, up rows I..2I-1). C = a b^T accumulated in fp32.
+//   mode 1 (SwiGLU, a hook only in the reference, design.md:107-109):
+//     d = bf16_RNE(silu(g) * u), g/u the fp32 accumulators, silu(x) = x/(1+e^-x);
+//     the C workspace is not written (the point of the fusion).
+//   modes 0/2/4/5/7/8: the workspace receives C = bf16_RNE(a b^T); d is the gate
+//   window (0, 5), the up window (4), nothing (2, 7) or zeros (8).
+//   mode 3: d = workspace[:, :I] (no GEMM).
+//
+// MI355X design:
+// * D^T = W X^T on v_mfma_f32_32x32x16_bf16: A operand = weight rows, B operand
+//   = activation rows, both K-contiguous in memory, so fragments are 16-byte
+//   LDS reads and each accumulator lane ends up holding 4 consecutive output
+//   columns (8-byte bf16 stores in the epilogue).
+// * Workgroup tile: 256 activation rows x (128 gate + the matching 128 up
+//   weight rows), K step 64, 8 waves arranged 2 (activation) x 4 (weight).
+//   Each wave owns 128 activation rows x (32 gate + 32 up) weight rows, so the
+//   gate and up accumulators of one output element sit in the same lane and
+//   register index: SwiGLU is computed in registers in fp32 and stored once as
+//   bf16 -- the gate/up product never reaches memory.
+// * Operand tiles go global -> registers -> LDS (double buffered, 2 x 64 KB,
+//   16-byte XOR swizzle per 128-byte row so the 32-row MFMA fragment reads are
+//   bank-conflict free); the next K tile's global loads are in flight while the
+//   current tile's 32 MFMAs per wave run.
+// * Tiles are ordered M-fastest and XCD-aware so the workgroups sharing a
+//   weight slice run on the same XCD and hit its L2.
+#include "ck_common.h"
+
+namespace ck {
+namespace {
+
+constexpr int kBM = 256;        // activation rows per workgroup
+constexpr int kBNh = 128;       // gate columns per workgroup (and as many up columns)
+constexpr int kBW = 2 * kBNh;   // weight rows staged per workgroup
+constexpr int kBK = 64;
+constexpr int kThreads = 512;
+constexpr int kRowBytes = kBK * 2;                // 128 B per staged row
+constexpr int kTileBytes = (kBM + kBW) * kRowBytes;  // 64 KB per stage
+constexpr int kChunksPerThread = (kBM + kBW) * (kBK / 8) / kThreads;  // 8
+
+struct GemmArgs {
+    const uint16_t *a;
+    const uint16_t *b;
+    uint16_t *c;
+    uint16_t *d;
+    int64_t m;
+    int64_t n_half;
+    int64_t k;
+    int64_t d_stride;
+    int mtiles;
+    int ntiles;
+};
+
+__device__ __forceinline__ int sw_off(int row, int c) { return row * kRowBytes + ((c ^ (row & 7)) << 4); }
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    const float e = exp2_fast(-g * kLog2e);
+    return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kThreads) void gateup_kernel(GemmArgs p) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int tid = threadIdx.x;
+    const int wid = tid >> 6;
+    const int lane = tid & 63;
+    const int hh = lane >> 5;
+    const int l32 = lane & 31;
+    const int wa = wid >> 2;  // activation half: rows wa*128 .. +128
+    const int ww = wid & 3;   // weight quarter: gate rows ww*32 .. +32 (and up)
+
+    const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
+    const int mi = w % p.mtiles;
+    const int ni = w / p.mtiles;
+    const int64_t m0 = (int64_t)mi * kBM;
+    const int64_t n0 = (int64_t)ni * kBNh;
+    const int ktiles = (int)((p.k + kBK - 1) / kBK);
+
+    // staging assignment: chunk ci = tid + 512u -> staged row ci/8, 16-byte chunk ci%8
+    const uint16_t *src[kChunksPerThread];
+    bool rvalid[kChunksPerThread];
+#pragma unroll
+    for (int u = 0; u < kChunksPerThread; ++u) {
+        const int ci = tid + kThreads * u;
+        const int row = ci >> 3, c = ci & 7;
+        if (row < kBM) {
+            const int64_t gm = m0 + row;
+            rvalid[u] = gm < p.m;
+            src[u] = p.a + (rvalid[u] ? gm : 0) * p.k + c * 8;
+        } else {
+            const int wr = row - kBM;
+            const int64_t gn = wr < kBNh ? n0 + wr : p.n_half + n0 + (wr - kBNh);
+            rvalid[u] = true;
+            src[u] = p.b + gn * p.k + c * 8;
+        }
+    }
+    uint4 stage[kChunksPerThread];
+    auto load_tile = [&](int kt) {
+        const int64_t k0 = (int64_t)kt * kBK;
+#pragma unroll
+        for (int u = 0; u < kChunksPerThread; ++u) {
+            const int c = (tid + kThreads * u) & 7;
+            const bool ok = rvalid[u] && (k0 + c * 8) < p.k;
+            stage[u] = ok ? *reinterpret_cast<const uint4 *>(src[u] + k0) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto store_tile = [&](int buf) {
+        char *base = smem + buf * kTileBytes;
+#pragma unroll
+        for (int u = 0; u < kChunksPerThread; ++u) {
+            const int ci = tid + kThreads * u;
+            *reinterpret_cast<uint4 *>(base + sw_off(ci >> 3, ci & 7)) = stage[u];
+        }
+    };
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int ab = 0; ab < 4; ++ab)
+#pragma unroll
+        for (int gu = 0; gu < 2; ++gu)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[ab][gu][e] = 0.f;
+
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+    if (ktiles > 1) load_tile(1);
+
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const char *xa = smem + (kt & 1) * kTileBytes;
+        const char *wb = xa + kBM * kRowBytes;
+#pragma unroll
+        for (int s = 0; s < kBK / 16; ++s) {
+            const int ch = 2 * s + hh;
+            bf16x8 wf[2], xf[4];
+            wf[0] = *reinterpret_cast<const bf16x8 *>(wb + sw_off(ww * 32 + l32, ch));
+            wf[1] = *reinterpret_cast<const bf16x8 *>(wb + sw_off(kBNh + ww * 32 + l32, ch));
+#pragma unroll
+            for (int ab = 0; ab < 4; ++ab)
+                xf[ab] = *reinterpret_cast<const bf16x8 *>(xa + sw_off(wa * 128 + ab * 32 + l32, ch));
+#pragma unroll
+            for (int ab = 0; ab < 4; ++ab)
+#pragma unroll
+                for (int gu = 0; gu < 2; ++gu)
+                    acc[ab][gu] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[gu], xf[ab], acc[ab][gu], 0, 0, 0);
+        }
+        if (kt + 1 < ktiles) store_tile((kt + 1) & 1);
+        __syncthreads();
+        if (kt + 2 < ktiles) load_tile(kt + 2);
+    }
+
+    // ---- epilogue: lane = activation row l32 of block ab; regs 4c..4c+3 =
+    // output columns n0 + ww*32 + 8c + 4hh + 0..3 --------------------------------
+#pragma unroll
+    for (int ab = 0; ab < 4; ++ab) {
+        const int64_t gm = m0 + wa * 128 + ab * 32 + l32;
+        if (gm >= p.m) continue;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int64_t col = n0 + ww * 32 + 8 * c + 4 * hh;
+            const float g0 = acc[ab][0][4 * c + 0], g1 = acc[ab][0][4 * c + 1];
+            const float g2 = acc[ab][0][4 * c + 2], g3 = acc[ab][0][4 * c + 3];
+            const float u0 = acc[ab][1][4 * c + 0], u1 = acc[ab][1][4 * c + 1];
+            const float u2 = acc[ab][1][4 * c + 2], u3 = acc[ab][1][4 * c + 3];
+            if (MODE == 1) {
+                const uint2 dv = make_uint2(pack_bf16x2(silu_mul(g0, u0), silu_mul(g1, u1)),
+                                            pack_bf16x2(silu_mul(g2, u2), silu_mul(g3, u3)));
+                *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = dv;
+            } else {
+                const uint2 gv = make_uint2(pack_bf16x2(g0, g1), pack_bf16x2(g2, g3));
+                const uint2 uv = make_uint2(pack_bf16x2(u0, u1), pack_bf16x2(u2, u3));
+                uint16_t *crow = p.c + gm * (2 * p.n_half);
+                *reinterpret_cast<uint2 *>(crow + col) = gv;
+                *reinterpret_cast<uint2 *>(crow + p.n_half + col) = uv;
+                if (MODE == 0 || MODE == 5)
+                    *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = gv;
+                else if (MODE == 4)
+                    *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = uv;
+                else if (MODE == 8)
+                    *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = make_uint2(0, 0);
+            }
+        }
+    }
+}
+
+// mode 3: d = workspace[:, :I] (epilogue-only rung), 8 columns per thread.
+__global__ __launch_bounds__(256) void gate_window_copy_kernel(const uint16_t *c, uint16_t *d, int64_t m,
+                                                               int64_t n_half, int64_t d_stride) {
+    const int64_t per_row = n_half / 8;
+    const int64_t total = m * per_row;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / per_row, q = i - r * per_row;
+        const uint4 v = *reinterpret_cast<const uint4 *>(c + r * 2 * n_half + q * 8);
+        uint16_t *dst = d + r * d_stride + q * 8;
+        // d_stride may be odd-aligned only to 8 bytes in general; store as 4 x 4 bytes
+        reinterpret_cast<uint2 *>(dst)[0] = make_uint2(v.x, v.y);
+        reinterpret_cast<uint2 *>(dst)[1] = make_uint2(v.z, v.w);
+    }
+}
+
+template <int MODE>
+int launch_gemm(const GemmArgs &p, hipStream_t s) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gateup_kernel<MODE>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kTileBytes);
+        if (e != hipSuccess) return static_cast<int>(e);
+        attr_set = true;
+    }
+    const int64_t grid = (int64_t)p.mtiles * p.ntiles;
+    hipLaunchKernelGGL((gateup_kernel<MODE>), dim3((unsigned)grid), dim3(kThreads), 2 * kTileBytes, s, p);
+    CK_RETURN_LAUNCH();
+}
+
+}  // namespace
+}  // namespace ck
+
+using namespace ck;
+
+extern "C" int ck_f3_gateup_epilogue(const void *a, const void *b, void *workspace, void *d, int64_t m,
+                                     int64_t n_half, int64_t k, int64_t mode, int64_t d_stride, void *stream) {
+    if (m < 1 || k < 64 || k % 16 != 0 || n_half < kBNh || n_half % kBNh != 0) return CK_E_INVALID_ARG;
+    if (!(mode >= 0 && mode <= 5) && mode != 7 && mode != 8) return CK_E_INVALID_ARG;
+    if (d_stride < n_half || d_stride % 4 != 0) return CK_E_INVALID_ARG;
+    if (!a || !b || !d) return CK_E_NULL_PTR;
+    if (mode != 1 && !workspace) return CK_E_NULL_PTR;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (mode == 3) {
+        int64_t blocks = (m * (n_half / 8) + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        hipLaunchKernelGGL(gate_window_copy_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                           static_cast<const uint16_t *>(workspace), static_cast<uint16_t *>(d), m, n_half,
+                           d_stride);
+        CK_RETURN_LAUNCH();
+    }
+    GemmArgs p;
+    p.a = static_cast<const uint16_t *>(a);
+    p.b = static_cast<const uint16_t *>(b);
+    p.c = static_cast<uint16_t *>(workspace);
+    p.d = static_cast<uint16_t *>(d);
+    p.m = m;
+    p.n_half = n_half;
+    p.k = k;
+    p.d_stride = d_stride;
+    p.mtiles = (int)((m + kBM - 1) / kBM);
+    p.ntiles = (int)(n_half / kBNh);
+    if ((int64_t)p.mtiles * p.ntiles > 0x7FFFFFFF) return CK_E_INVALID_ARG;
+    switch (mode) {
+        case 0: return launch_gemm<0>(p, s);
+        case 1: return launch_gemm<1>(p, s);
+        case 2: return launch_gemm<2>(p, s);
+        case 4: return launch_gemm<4>(p, s);
+        case 5: return launch_gemm<5>(p, s);
+        case 7: return launch_gemm<7>(p, s);
+        default: return launch_gemm<8>(p, s);
+    }
+}
