@@ -1,0 +1,243 @@
+"""Benchmark of the cascade-decode operator set on one MI355X.
+
+Workload (BASELINE config 2 end-to-end, plus config 4 at M=4096):
+  * cascade decode, Llama-3-8B attention shapes: 32 query heads, 8 kv heads,
+    head dim 128, bf16; a shared 8192-token prefix (64 pages of 128 tokens,
+    permuted physical pages) read by stage-1 in the flattened form (one request,
+    q_len = 64); 64 sequences whose own suffixes have geometric lengths (mean 512,
+    clipped to [1, 4096]) read by suffix_decode; the two partial results merged
+    by lse_merge into bf16. One step = these three ops.
+  * the fused SwiGLU gate_up GEMM, activations [4096, 4096], weight
+    [2*14336, 4096] bf16, fp32 accumulation, d = silu(g) * u in bf16.
+
+value = end-to-end cascade HBM throughput: algorithmic bytes (q, prefix K/V read
+once, every suffix K/V, block tables, seqlens, final bf16 O) / measured time of
+the three ops. Inputs are resident in HBM; K/V pools rotate through enough copies
+(>= 2 GiB distinct) that the 256 MB Infinity Cache cannot serve them.
+Every timed op is bracketed by HIP events on the stream the kernels run on.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "vllm-hust-cascade-kernel_amd"))
+
+HBM_PEAK_GBS = 8000.0        # MI355X published HBM3E bandwidth
+BF16_PEAK_TFLOPS = 2500.0    # MI355X published dense bf16 MFMA peak
+
+B, H, KVH, D, PREFIX, PAGE = 64, 32, 8, 128, 8192, 128
+GEMM_M, GEMM_K, GEMM_I = 4096, 4096, 14336
+ROTATE_BYTES = 2 << 30
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def suffix_lengths():
+    import numpy as np
+    rng = np.random.default_rng(0)
+    return np.clip(rng.geometric(1.0 / 512, size=B), 1, 4096).astype(np.int64)
+
+
+def build_workload(torch, dev):
+    import numpy as np
+    suf = suffix_lengths()
+    nsb = [(int(s) + PAGE - 1) // PAGE for s in suf]
+    npages = PREFIX // PAGE + sum(nsb)
+    rng = np.random.default_rng(1)
+    perm = rng.permutation(npages).astype(np.int32)
+    bt_pre = torch.from_numpy(perm[:PREFIX // PAGE][None, :].copy()).to(dev)
+    bt_suf_np = np.zeros((B, max(nsb)), dtype=np.int32)
+    off = PREFIX // PAGE
+    for b in range(B):
+        bt_suf_np[b, :nsb[b]] = perm[off:off + nsb[b]]
+        off += nsb[b]
+    bt_suf = torch.from_numpy(bt_suf_np).to(dev)
+    pool_bytes = 2 * npages * PAGE * KVH * D * 2
+    copies = max(2, -(-ROTATE_BYTES // pool_bytes))
+    g = torch.Generator(device=dev).manual_seed(0)
+    pools = []
+    for _ in range(copies):
+        k = torch.randn(npages, PAGE, KVH, D, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        v = torch.randn(npages, PAGE, KVH, D, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        q = torch.randn(B, H, D, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        pools.append((q, k, v))
+    w = dict(
+        pools=pools, bt_pre=bt_pre, bt_suf=bt_suf,
+        qlens=torch.tensor([B], dtype=torch.int64, device=dev),
+        kvlens=torch.tensor([PREFIX], dtype=torch.int64, device=dev),
+        suf=torch.from_numpy(suf).to(dev), suf_np=suf, npages=npages, copies=copies,
+    )
+    # algorithmic bytes of one cascade step (inputs read once, final output written once)
+    kv_tok = KVH * D * 2 * 2
+    w["bytes_prefix_kernel"] = (B * H * D * 2 + PREFIX * kv_tok + bt_pre.numel() * 4 + 16
+                                + B * H * D * 4 + B * H * 8 * 4)       # stage-1 reads + fp32 O + padded LSE
+    w["bytes_suffix_kernel"] = (B * H * D * 2 + int(suf.sum()) * kv_tok + bt_suf.numel() * 4 + B * 8
+                                + B * H * D * 2 + B * H * 4)            # suffix reads + bf16 O + LSE
+    w["bytes_merge_kernel"] = B * H * D * (4 + 2 + 2) + B * H * (8 + 1) * 4
+    w["bytes_end_to_end"] = (B * H * D * 2 + PREFIX * kv_tok + int(suf.sum()) * kv_tok
+                             + (bt_pre.numel() + bt_suf.numel()) * 4 + 2 * B * 8 + B * H * D * 2)
+    w["flops_prefix"] = 4 * B * H * D * PREFIX
+    return w
+
+
+def cpu_baseline(torch):
+    """Times the CPU oracle (numpy restatement, test infrastructure) on one full
+    cascade step of the same workload: einsum loops, one thread."""
+    import numpy as np
+    sys.path.insert(0, REPO)
+    from oracle import attention as A
+    from oracle.merge import merge_fp64
+    suf = suffix_lengths()
+    rng = np.random.default_rng(2)
+    nsb = [(int(s) + PAGE - 1) // PAGE for s in suf]
+    npages = PREFIX // PAGE + sum(nsb)
+    k = rng.standard_normal((npages, PAGE, KVH, D)).astype(np.float32)
+    v = rng.standard_normal((npages, PAGE, KVH, D)).astype(np.float32)
+    q = rng.standard_normal((B, H, D)).astype(np.float32)
+    bt_pre = np.arange(PREFIX // PAGE, dtype=np.int32)[None]
+    bt_suf = np.zeros((B, max(nsb)), dtype=np.int32)
+    off = PREFIX // PAGE
+    for b in range(B):
+        bt_suf[b, :nsb[b]] = np.arange(off, off + nsb[b])
+        off += nsb[b]
+    t0 = time.perf_counter()
+    O1, L1 = A.stage1(q, k, v, bt_pre, [B], [PREFIX])
+    O2, L2 = A.suffix(q, k, v, bt_suf, suf)
+    merge_fp64(O1, O2, L1, L2)
+    dt = time.perf_counter() - t0
+    kv_tok = KVH * D * 2 * 2
+    nbytes = B * H * D * 2 + PREFIX * kv_tok + int(suf.sum()) * kv_tok + B * H * D * 2
+    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": "one full cascade step of the benchmark workload (stage-1 + suffix + merge) "
+                      "through the numpy oracle, %.1f s" % dt}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU; --gpus %d is not supported "
+              "(the cascade-decode path shards by kv head with no exchange; see DESIGN.md)" % args.gpus,
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import cascade_amd  # noqa: F401
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+
+    w = build_workload(torch, dev)
+    a = torch.randn(GEMM_M, GEMM_K, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    wt = (torch.randn(2 * GEMM_I, GEMM_K, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+    d_out = torch.empty(GEMM_M, GEMM_I, device=dev, dtype=torch.bfloat16)
+    ws = torch.empty(GEMM_M, 2 * GEMM_I, device=dev, dtype=torch.bfloat16)
+
+    # calibration copy of known size (read 256 MiB + write 256 MiB) for the PMC
+    # traffic scale factor; outside the timed region
+    src = torch.empty(128 << 20, dtype=torch.int16, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+    def step(i, ev=None):
+        q, k, v = w["pools"][i % w["copies"]]
+        if ev is not None:
+            ev[0].record(stream)
+        o1, l1 = torch.ops.npu.fa_fp32_stage1(q, k, v, w["bt_pre"], w["qlens"], w["kvlens"], B)
+        if ev is not None:
+            ev[1].record(stream)
+        o2, l2 = torch.ops.npu.suffix_decode(q, k, v, w["bt_suf"], w["suf"])
+        if ev is not None:
+            ev[2].record(stream)
+        torch.ops.npu.lse_merge(o1, o2, l1, l2, 1)
+        if ev is not None:
+            ev[3].record(stream)
+        torch.ops.npu.f3_gateup_epilogue(a, wt, ws, d_out, 1)
+        if ev is not None:
+            ev[4].record(stream)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i, evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    ms = {"stage1": 0.0, "suffix": 0.0, "merge": 0.0, "cascade": 0.0, "gemm": 0.0}
+    for e in evs:
+        ms["stage1"] += e[0].elapsed_time(e[1])
+        ms["suffix"] += e[1].elapsed_time(e[2])
+        ms["merge"] += e[2].elapsed_time(e[3])
+        ms["cascade"] += e[0].elapsed_time(e[3])
+        ms["gemm"] += e[3].elapsed_time(e[4])
+    for k_ in ms:
+        ms[k_] /= args.steps
+
+    cascade_gbs = w["bytes_end_to_end"] / (ms["cascade"] * 1e-3) / 1e9
+    gemm_flops = 2.0 * GEMM_M * GEMM_K * 2 * GEMM_I
+    gemm_tflops = gemm_flops / (ms["gemm"] * 1e-3) / 1e12
+    per_kernel = {
+        "fa_fp32_stage1": (ms["stage1"], w["bytes_prefix_kernel"]),
+        "suffix_decode": (ms["suffix"], w["bytes_suffix_kernel"]),
+        "lse_merge": (ms["merge"], w["bytes_merge_kernel"]),
+    }
+    dom = max(per_kernel, key=lambda n: per_kernel[n][0])
+    dom_gbs = per_kernel[dom][1] / (per_kernel[dom][0] * 1e-3) / 1e9
+    traffic = None
+    tpath = os.path.join(REPO, "profiles", "pmc_traffic.json")
+    if os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get(dom)
+
+    line = {
+        "metric": "cascade-decode attn HBM GB/s (% of peak) + SwiGLU GEMM TFLOP/s at 1 MI355X",
+        "value": round(cascade_gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1) bf16 q/k/v, N(0,0.02) weights, seeded)",
+        "config": {
+            "workload": "cascade decode H32/KVH8/D128, shared prefix 8192 (flattened stage-1, q_len 64), "
+                        "64 suffixes ~Geometric(mean 512) clipped [1,4096] (%d tokens), page 128, permuted "
+                        "pages, merge to bf16; plus fused SwiGLU gate_up GEMM M=%d K=%d I=%d"
+                        % (int(w["suf_np"].sum()), GEMM_M, GEMM_K, GEMM_I),
+            "kv_rotation_copies": w["copies"],
+        },
+        "cascade_pct_of_hbm_peak": round(100.0 * cascade_gbs / HBM_PEAK_GBS, 2),
+        "cascade_us": round(ms["cascade"] * 1e3, 2),
+        "per_op_us": {n: round(v[0] * 1e3, 2) for n, v in per_kernel.items()},
+        "swiglu_gemm": {"tflops": round(gemm_tflops, 1), "us": round(ms["gemm"] * 1e3, 1),
+                        "pct_of_bf16_peak": round(100.0 * gemm_tflops / BF16_PEAK_TFLOPS, 2)},
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(dom_gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "roofline_gemm": {"kernel": "f3_gateup_epilogue mode 1", "bound": "mfma", "achieved": round(gemm_tflops, 1),
+                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                          "frac": round(gemm_tflops / BF16_PEAK_TFLOPS, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(torch)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -29,7 +29,7 @@ KERNEL_SOURCES = ["abi.hip", "lse_merge.hip", "fa_stage1.hip", "suffix_decode.hi
 
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fno-gpu-rdc",
-    "-munsafe-fp-atomics", "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
+    "-munsafe-fp-atomics", "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-inline-asm",
     # Packed FP32 ops (v_pk_*_f32) are disabled for all device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}", f"-I{CSRC}",

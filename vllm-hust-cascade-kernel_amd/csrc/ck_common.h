@@ -14,6 +14,7 @@ namespace ck {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(unsigned)))) unsigned u32x4;
 
 constexpr int kWave = 64;
 constexpr int kNumXcd = 8;
@@ -31,8 +32,45 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
     if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) | 0x40u) & 0xFFFFu;
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
+// Two floats -> packed bf16 pair, round to nearest even (one v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+    const bf16x2v v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+#define CK_LDS __attribute__((address_space(3)))
+
+// 16-byte global -> LDS DMA (gfx950 global_load_lds_dwordx4): lane l's 16 bytes
+// land at lds_base + 16 * l; lds_base must be wave-uniform. Issued as inline asm
+// so the compiler does not guard every later LDS read with a vmcnt(0) wait (it
+// cannot prove transpose reads do not alias the DMA); callers wait explicitly
+// with wait_vmcnt<N>() and a workgroup barrier before reading the data.
+__device__ __forceinline__ void dma16(const void *g, CK_LDS void *lds_base) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_base);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(m0), "v"(g)
+                 : "memory", "m0");
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding
+// (gfx9 s_waitcnt encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS transpose read (gfx950 ds_read_b64_tr_b16). Within each 16-lane group,
+// result lane i receives element (i % 4) of the 8-byte rows addressed by source
+// lanes i/4, i/4+4, i/4+8, i/4+12. A group that addresses a 4-token x 16-element
+// block (lane s -> token s/4, elements 4(s%4)..+3) therefore gets element i of
+// the 4 tokens in lane i.
+__device__ __forceinline__ uint2 lds_read_tr16(const CK_LDS char *p) {
+    typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
+    s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((CK_LDS s16x4 *)p);
+    return __builtin_bit_cast(uint2, v);
 }
 
 // 2^x on the hardware exp unit.

@@ -17,21 +17,28 @@
 //   head g*group + r % group), so the GQA group and every query of the request
 //   that shares the prefix ride in the same MFMA tile: the flattened cascade
 //   form (one request, q_len = batch) reads each prefix page once per m-tile.
-// * One workgroup = 4 waves x 32 query rows. K and V^T tiles of 64 tokens are
-//   staged through double-buffered LDS (2 x 32 KB); each wave keeps its Q rows
+// * One workgroup = 128 query rows x one kv split, run by 8 waves: wave w owns
+//   query rows 32*(w%4) .. +32 and token half w/4 of every 64-token tile, with
+//   its own online-softmax state; the two halves merge through LDS at the end.
+//   Two waves per SIMD let one wave's softmax VALU overlap the other's MFMAs.
+//   K and V tiles stream into a 4-stage LDS ring (4 x 32 KB) by global->LDS DMA
+//   (global_load_lds, 16 B per lane): no staging registers, three tiles in
+//   flight while one is computed. The split's page ids are read once into LDS,
+//   so no load in the loop depends on another load. Each wave keeps its Q rows
 //   as MFMA operands in registers for the whole kv loop.
 // * S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (A = K rows from LDS, B = Q); the
 //   accumulator layout puts one query row per lane, so row max / row sum need a
 //   single cross-half exchange. P^T leaves the accumulator directly as the B
-//   operand of O^T += V^T P^T; the MFMA's k order (tokens 0-3,8-11 | 4-7,12-15
-//   per 16) is matched by storing V^T in LDS with that token permutation.
-// * V is transposed in registers (4 tokens x 8 dims per thread) on its way to
-//   LDS; K and V^T rows are XOR-swizzled at 16-byte granularity so the MFMA
-//   fragment reads are bank-conflict free.
+//   operand of O^T += V^T P^T; the V^T operand comes from the untransposed V
+//   tile through ds_read_b64_tr_b16, two reads per fragment, whose token order
+//   (0-3, 8-11 | 4-7, 12-15 per 16) is the accumulator's own.
+// * K and V rows are XOR-swizzled at 16-byte granularity (chunk ^ token) by
+//   choosing which global chunk each DMA lane fetches, so MFMA fragment reads
+//   and transpose reads are bank-conflict free.
 // * Softmax runs in the log2 domain (exp2 on the hardware unit, S pre-scaled by
 //   scale*log2(e)); LSE is converted back to natural log.
 // * Split-KV fills the chip when batch*kv_heads*m-tiles is small; partial
-//   (O, LSE) pairs are folded by an N-way LSE merge (ck_stage1_combine).
+//   (O, LSE) pairs are folded by an N-way LSE merge (stage1_combine_kernel).
 // * Block order is XCD-aware: the m-tiles that read the same kv pages are
 //   placed on the same XCD so the second read hits that XCD's L2.
 #include "ck_common.h"
@@ -42,12 +49,15 @@ namespace {
 constexpr int kD = 128;          // head dim (op contract)
 constexpr int kPage = 128;       // paged block size (op contract)
 constexpr int kTileN = 64;       // kv tokens per tile
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * kWave;
-constexpr int kRows = 32 * kWaves;  // query rows per workgroup
-constexpr int kKTileBytes = kTileN * kD * 2;  // 16 KB
-constexpr int kVTileBytes = kD * kTileN * 2;  // 16 KB
-constexpr int kBufBytes = kKTileBytes + kVTileBytes;
+constexpr int kRows = 128;          // query rows per workgroup (4 row blocks x 2 token halves)
+constexpr int kStages = 4;          // LDS ring depth
+constexpr int kTileBytes = kTileN * kD * 2;   // 16 KB for K, the same for V
+constexpr int kStageBytes = 2 * kTileBytes;
+constexpr int kMaxSplitPages = 256;           // page ids held in LDS per split
+constexpr int kLdsBytes = kStages * kStageBytes + kMaxSplitPages * 4;
+constexpr int kDmaPerTile = 2 * (kTileBytes / 1024) / kWaves;  // 16-B-per-lane DMAs per wave per tile (4)
 
 struct Stage1Args {
     const uint16_t *q;
@@ -76,10 +86,6 @@ struct Stage1Args {
     float scale_log2;
 };
 
-__device__ __forceinline__ bf16x8 lds_read16(const char *p) {
-    return *reinterpret_cast<const bf16x8 *>(p);
-}
-
 __device__ __forceinline__ bf16x8 pack_p(const f32x16 &s, int base) {
     uint4 w;
     w.x = pack_bf16x2(s[base + 0], s[base + 1]);
@@ -89,21 +95,27 @@ __device__ __forceinline__ bf16x8 pack_p(const f32x16 &s, int base) {
     return __builtin_bit_cast(bf16x8, w);
 }
 
-// Byte offset of K[token][16-byte chunk c] in a K tile.
-__device__ __forceinline__ int k_off(int tok, int c) { return tok * (kD * 2) + ((c ^ (tok & 15)) << 4); }
+// Byte offset of row tok, 16-byte chunk c inside a K or V tile (XOR swizzle).
+__device__ __forceinline__ int tile_off(int tok, int c) { return tok * (kD * 2) + ((c ^ (tok & 15)) << 4); }
 
-// Byte offset of the 16-byte chunk ch (token positions 8ch..8ch+7) of V^T row dim.
-__device__ __forceinline__ int vt_off(int dim, int ch) {
-    return dim * (kTileN * 2) + ((ch ^ ((dim ^ (dim >> 3)) & 7)) << 4);
+__device__ __forceinline__ void wait_tiles(int outstanding) {
+    // at most `outstanding` later tiles (kDmaPerTile DMAs each) may remain in flight
+    if (outstanding >= 2) wait_vmcnt<2 * kDmaPerTile>();
+    else if (outstanding == 1) wait_vmcnt<kDmaPerTile>();
+    else wait_vmcnt<0>();
 }
 
 __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
-    __shared__ __attribute__((aligned(16))) char smem[2 * kBufBytes];
+    extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+    CK_LDS char *smem = (CK_LDS char *)smem_raw;
+    CK_LDS int *s_pages = (CK_LDS int *)(smem + kStages * kStageBytes);
 
     const int tid = threadIdx.x;
     const int wid = tid >> 6;
     const int lane = tid & 63;
     const int hh = lane >> 5;
+    const int rb = wid & 3;   // row block
+    const int th = wid >> 2;  // token half of each tile
 
     uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
     const int mt = w % a.mtiles;
@@ -129,13 +141,20 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
     const int64_t kv_lim = a.bt_cols * kPage;
     if (kvl > kv_lim) kvl = kv_lim;
     if (kvl > a.kv_cap) kvl = a.kv_cap;
-    if (kvl < 0) kvl = 0;
-    const int kv_lo = sp * a.split_len;
+    if (kvl < 0 || a.num_blocks <= 0) kvl = 0;  // no pool: nothing to attend to
+    const int kv_lo = sp * a.split_len;  // a multiple of kPage
     int kv_hi = kv_lo + a.split_len;
     if (kv_hi > (int)kvl) kv_hi = (int)kvl;
     const int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + kTileN - 1) / kTileN : 0;
 
-    const int wrow0 = row0 + wid * 32;
+    // page ids of this split -> LDS (one load per page, before any K/V traffic)
+    const int npages = kv_hi > kv_lo ? (kv_hi - kv_lo + kPage - 1) / kPage : 0;
+    for (int pi = tid; pi < npages; pi += kThreads) {
+        const int page = a.bt[(int64_t)b * a.bt_cols + kv_lo / kPage + pi];
+        s_pages[pi] = (page >= 0 && (int64_t)page < a.num_blocks) ? page : -1;
+    }
+
+    const int wrow0 = row0 + rb * 32;
     const bool wave_active = wrow0 < rows_b;
     const int r = wrow0 + (lane & 31);
     const bool row_valid = r < rows_b;
@@ -153,75 +172,37 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
             qf[kk] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
         }
     }
+    // Q and page ids must be resident before the DMA ring starts: the compiler
+    // does not count the inline-asm DMAs, so a wait it deferred into the loop
+    // would also drain every tile in flight.
+    wait_vmcnt<0>();
+    __syncthreads();  // s_pages visible
 
-    // ---- tile staging: global -> registers -> LDS --------------------------------
-    constexpr int KU = (kTileN * kD / 8) / kThreads;  // 16-byte K chunks per thread
-    constexpr int VU = (kTileN / 4 * kD / 8) / kThreads;  // (4 tokens x 8 dims) V units per thread
-    uint4 kreg[KU];
-    uint4 vreg[VU][4];
     const int64_t head_stride = (int64_t)a.kv_heads * kD;
+    // DMA lane geometry: one wave instruction moves 4 token rows (1 KB); lane ->
+    // token 4*blk + lane/16 and LDS chunk lane%16, which holds global chunk
+    // (lane%16) ^ (token & 15).
+    const int dma_tt = lane >> 4;
+    const int dma_pc = lane & 15;
 
-    auto load_tile = [&](int i) {
+    auto issue_tile = [&](int i) {
         const int j0 = kv_lo + i * kTileN;
-        const int nvalid = min(kTileN, kv_hi - j0);
-        const int page = a.bt[(int64_t)b * a.bt_cols + (j0 / kPage)];
-        const bool pvalid = page >= 0 && (int64_t)page < a.num_blocks;
+        // an invalid page is zero-filled at wait time; its DMAs still go out (from
+        // page 0) so every wave keeps exactly kDmaPerTile operations per tile and
+        // the vmcnt-based waits stay exact
+        const int raw_page = s_pages[(j0 - kv_lo) / kPage];
+        const int page = raw_page < 0 ? 0 : raw_page;
+        CK_LDS char *kb = smem + (i % kStages) * kStageBytes;
+        CK_LDS char *vb = kb + kTileBytes;
         const int64_t tok0 = (int64_t)page * kPage + (j0 % kPage);
-        const uint4 zero = make_uint4(0, 0, 0, 0);
 #pragma unroll
-        for (int u = 0; u < KU; ++u) {
-            const int ci = tid + kThreads * u;
-            const int tt = ci >> 4, c = ci & 15;
-            kreg[u] = (pvalid && tt < nvalid)
-                          ? *reinterpret_cast<const uint4 *>(a.k + (tok0 + tt) * head_stride + g * kD + c * 8)
-                          : zero;
-        }
-#pragma unroll
-        for (int u = 0; u < VU; ++u) {
-            const int ui = tid + kThreads * u;
-            const int qd = ui >> 4, c = ui & 15;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int tt = qd * 4 + j;
-                vreg[u][j] = (pvalid && tt < nvalid)
-                                 ? *reinterpret_cast<const uint4 *>(a.v + (tok0 + tt) * head_stride + g * kD + c * 8)
-                                 : zero;
-            }
-        }
-    };
-
-    auto store_tile = [&](int buf) {
-        char *kb = smem + buf * kBufBytes;
-        char *vb = kb + kKTileBytes;
-#pragma unroll
-        for (int u = 0; u < KU; ++u) {
-            const int ci = tid + kThreads * u;
-            const int tt = ci >> 4, c = ci & 15;
-            *reinterpret_cast<uint4 *>(kb + k_off(tt, c)) = kreg[u];
-        }
-#pragma unroll
-        for (int u = 0; u < VU; ++u) {
-            const int ui = tid + kThreads * u;
-            const int qd = ui >> 4, c = ui & 15;
-            // token quad qd -> permuted position quad inside its 16-token group
-            const int qg = qd & 3;
-            const int p = (qd >> 2) * 16 + ((((qg & 1) << 1) | (qg >> 1)) << 2);
-            const uint32_t *t0 = reinterpret_cast<const uint32_t *>(&vreg[u][0]);
-            const uint32_t *t1 = reinterpret_cast<const uint32_t *>(&vreg[u][1]);
-            const uint32_t *t2 = reinterpret_cast<const uint32_t *>(&vreg[u][2]);
-            const uint32_t *t3 = reinterpret_cast<const uint32_t *>(&vreg[u][3]);
-#pragma unroll
-            for (int jw = 0; jw < 4; ++jw) {
-                // dims 2jw (low halves) and 2jw+1 (high halves) of tokens 0..3
-                const uint2 lo = make_uint2((t0[jw] & 0xFFFFu) | (t1[jw] << 16),
-                                            (t2[jw] & 0xFFFFu) | (t3[jw] << 16));
-                const uint2 hi = make_uint2((t0[jw] >> 16) | (t1[jw] & 0xFFFF0000u),
-                                            (t2[jw] >> 16) | (t3[jw] & 0xFFFF0000u));
-                const int d0 = c * 8 + 2 * jw;
-                const int ch = p >> 3, half = (p & 7) * 2;
-                *reinterpret_cast<uint2 *>(vb + vt_off(d0, ch) + half) = lo;
-                *reinterpret_cast<uint2 *>(vb + vt_off(d0 + 1, ch) + half) = hi;
-            }
+        for (int j = 0; j < kDmaPerTile / 2; ++j) {
+            const int blk = wid * (kDmaPerTile / 2) + j;
+            const int tt = blk * 4 + dma_tt;
+            const int c = dma_pc ^ (tt & 15);
+            const int64_t off = (tok0 + tt) * head_stride + g * kD + c * 8;
+            dma16(a.k + off, kb + blk * 1024);
+            dma16(a.v + off, vb + blk * 1024);
         }
     };
 
@@ -234,82 +215,129 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
     float m_run = -INFINITY;
     float l_run = 0.f;
 
-    if (ntiles > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
-    __syncthreads();
-    if (ntiles > 1) load_tile(1);
+    for (int i = 0; i < kStages - 1 && i < ntiles; ++i) issue_tile(i);
+
+    // per-lane LDS offsets (loop invariant): K fragment rows of this token half,
+    // and the V^T transpose-read addresses. Transpose reads: lane group
+    // G = lane/16 covers dims 16*(G%2) + 0..15 of each 32-dim block and the
+    // token quad 4*(G/2); its source lane s addresses token s/4, dims 4*(s%4)..+3.
+    const int ktok = th * 32 + (lane & 31);
+    const int trG = (lane >> 4) & 3;
+    const int tr_row = (lane & 15) >> 2;
+    const int tr_e4 = lane & 3;
 
     for (int i = 0; i < ntiles; ++i) {
-        if (wave_active) {
-            const char *kb = smem + (i & 1) * kBufBytes;
-            const char *vb = kb + kKTileBytes;
-            const int nvalid = min(kTileN, kv_hi - (kv_lo + i * kTileN));
-            f32x16 sacc[2];
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb) {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) sacc[tb][e] = 0.f;
-                const int tok = tb * 32 + (lane & 31);
-#pragma unroll
-                for (int kk = 0; kk < 8; ++kk) {
-                    const bf16x8 kf = lds_read16(kb + k_off(tok, 2 * kk + hh));
-                    sacc[tb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sacc[tb], 0, 0, 0);
-                }
+        const int outstanding = min(kStages - 2, ntiles - 1 - i);
+        wait_tiles(outstanding);
+        __syncthreads();
+        const int j0 = kv_lo + i * kTileN;
+        const int nvalid = min(kTileN, kv_hi - j0);
+        const bool page_ok = s_pages[(j0 - kv_lo) / kPage] >= 0;
+        CK_LDS char *kb = smem + (i % kStages) * kStageBytes;
+        CK_LDS char *vb = kb + kTileBytes;
+        if (nvalid < kTileN || !page_ok) {
+            // rows past the sequence end (or of an invalid page) may hold
+            // anything: zero them so 0 * V cannot produce a NaN
+            const int z0 = page_ok ? nvalid : 0;
+            for (int idx = tid; idx < (kTileN - z0) * 16; idx += kThreads) {
+                const int tt = z0 + (idx >> 4), c = idx & 15;
+                *reinterpret_cast<CK_LDS u32x4 *>(kb + tt * 256 + c * 16) = u32x4{0, 0, 0, 0};
+                *reinterpret_cast<CK_LDS u32x4 *>(vb + tt * 256 + c * 16) = u32x4{0, 0, 0, 0};
             }
-            // scale, mask, row max
-            float smax = -INFINITY;
+            __syncthreads();
+        }
+        if (i + kStages - 1 < ntiles) issue_tile(i + kStages - 1);
+
+        if (wave_active && th * 32 < nvalid) {
+            f32x16 sacc;
 #pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
+            for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const bf16x8 kf = *reinterpret_cast<const CK_LDS bf16x8 *>(kb + tile_off(ktok, 2 * kk + hh));
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sacc, 0, 0, 0);
+            }
+            // scale (log2 domain), mask only on a partial tile, row max
+            float smax = -INFINITY;
+            if (nvalid < kTileN) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const int tok = tb * 32 + (e & 3) + 8 * (e >> 2) + 4 * hh;
-                    float s = sacc[tb][e] * a.scale_log2;
-                    s = tok < nvalid ? s : -INFINITY;
-                    sacc[tb][e] = s;
-                    smax = fmaxf(smax, s);
+                    const int tok = th * 32 + (e & 3) + 8 * (e >> 2) + 4 * hh;
+                    const float sv = tok < nvalid ? sacc[e] * a.scale_log2 : -INFINITY;
+                    sacc[e] = sv;
+                    smax = fmaxf(smax, sv);
                 }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    sacc[e] *= a.scale_log2;
+                    smax = fmaxf(smax, sacc[e]);
+                }
+            }
             smax = fmaxf(smax, __shfl_xor(smax, 32));
             const float m_new = fmaxf(m_run, smax);
             const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
             const float dm = exp2_fast(m_run - m_use);
             float ls = 0.f;
 #pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const float p = exp2_fast(sacc[tb][e] - m_use);
-                    sacc[tb][e] = p;
-                    ls += p;
-                }
+            for (int e = 0; e < 16; ++e) {
+                const float p = exp2_fast(sacc[e] - m_use);
+                sacc[e] = p;
+                ls += p;
+            }
             ls += __shfl_xor(ls, 32);
             l_run = l_run * dm + ls;
             m_run = m_new;
+            // rescale only when some row's max moved (wave-uniform branch)
+            if (__builtin_amdgcn_ballot_w64(dm != 1.0f)) {
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
+                for (int db = 0; db < 4; ++db)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) oacc[db][e] *= dm;
-            // O^T += V^T P^T over 4 k-steps of 16 tokens
+                    for (int e = 0; e < 16; ++e) oacc[db][e] *= dm;
+            }
+            // O^T += V^T P^T over this half's 2 k-steps of 16 tokens
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const bf16x8 pb = pack_p(sacc[s >> 1], (s & 1) * 8);
+            for (int ss = 0; ss < 2; ++ss) {
+                const int s = 2 * th + ss;
+                const bf16x8 pb = pack_p(sacc, ss * 8);
+                const int t1 = 16 * s + 4 * (trG >> 1) + tr_row;  // first read; second is t1 + 8
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
-                    const int dim = db * 32 + (lane & 31);
-                    const bf16x8 vf = lds_read16(vb + vt_off(dim, 2 * s + hh));
+                    const int d = 32 * db + 16 * (trG & 1) + 4 * tr_e4;  // 4 dims this lane addresses
+                    const int c = d >> 3, half = (d & 7) * 2;
+                    const uint2 lo = lds_read_tr16(vb + tile_off(t1, c) + half);
+                    const uint2 hi = lds_read_tr16(vb + tile_off(t1 + 8, c) + half);
+                    const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
                     oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb, oacc[db], 0, 0, 0);
                 }
             }
         }
-        if (i + 1 < ntiles) store_tile((i + 1) & 1);
-        __syncthreads();
-        if (i + 2 < ntiles) load_tile(i + 2);
     }
 
-    if (!row_valid) return;
-    const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
-    const float lse_v = l_run > 0.f ? (m_run + __log2f(l_run)) * kLn2 : -INFINITY;
+    // ---- merge the two token halves through LDS (the ring is free now) ----------------
+    __syncthreads();
+    CK_LDS float *xo = (CK_LDS float *)smem;               // [4 rb][16 quads][64 lanes][4]
+    CK_LDS float *xm = xo + 4 * 64 * 64;                   // [4 rb][64 lanes]
+    CK_LDS float *xl = xm + 4 * 64;
+    if (th == 1) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4)
+                *reinterpret_cast<CK_LDS f32x4 *>(xo + ((rb * 16 + db * 4 + c4) * 64 + lane) * 4) =
+                    f32x4{oacc[db][4 * c4], oacc[db][4 * c4 + 1], oacc[db][4 * c4 + 2], oacc[db][4 * c4 + 3]};
+        xm[rb * 64 + lane] = m_run;
+        xl[rb * 64 + lane] = l_run;
+    }
+    __syncthreads();
+    if (th == 1 || !row_valid) return;
+    const float m1 = xm[rb * 64 + lane], l1 = xl[rb * 64 + lane];
+    const float mn = fmaxf(m_run, m1);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float f0 = exp2_fast(m_run - mu), f1 = exp2_fast(m1 - mu);
+    const float lt = l_run * f0 + l1 * f1;
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    const float lse_v = lt > 0.f ? (mn + __log2f(lt)) * kLn2 : -INFINITY;
     float *dst;
     if (a.num_splits == 1) {
         dst = a.out + qrow * kD;
@@ -323,14 +351,18 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const float4 o = make_float4(oacc[db][4 * c + 0] * inv, oacc[db][4 * c + 1] * inv,
-                                         oacc[db][4 * c + 2] * inv, oacc[db][4 * c + 3] * inv);
-            *reinterpret_cast<float4 *>(dst + db * 32 + 8 * c + 4 * hh) = o;
+        for (int c4 = 0; c4 < 4; ++c4) {
+            const f32x4 o1 = *reinterpret_cast<const CK_LDS f32x4 *>(xo + ((rb * 16 + db * 4 + c4) * 64 + lane) * 4);
+            const float4 o = make_float4((oacc[db][4 * c4 + 0] * f0 + o1[0] * f1) * inv,
+                                         (oacc[db][4 * c4 + 1] * f0 + o1[1] * f1) * inv,
+                                         (oacc[db][4 * c4 + 2] * f0 + o1[2] * f1) * inv,
+                                         (oacc[db][4 * c4 + 3] * f0 + o1[3] * f1) * inv);
+            *reinterpret_cast<float4 *>(dst + db * 32 + 8 * c4 + 4 * hh) = o;
         }
 }
 
-// N-way LSE merge of split partials: 32 threads per row, 4 dims each.
+// N-way LSE merge of split partials: 32 threads per row, 4 dims each. Partials
+// are fetched four splits at a time with independent loads.
 __global__ __launch_bounds__(256) void stage1_combine_kernel(const float *part_o, const float *part_lse,
                                                              int num_splits, int64_t rows,
                                                              float *out, float *lse) {
@@ -339,20 +371,36 @@ __global__ __launch_bounds__(256) void stage1_combine_kernel(const float *part_o
     if (row >= rows) return;
     float m = -INFINITY;
     for (int s = 0; s < num_splits; ++s) m = fmaxf(m, part_lse[(int64_t)s * rows + row]);
+    const float mu = m == -INFINITY ? 0.f : m;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     float wsum = 0.f;
-    if (m != -INFINITY) {
-        for (int s = 0; s < num_splits; ++s) {
-            const float ls = part_lse[(int64_t)s * rows + row];
-            const float wgt = exp2_fast((ls - m) * kLog2e);
-            if (wgt == 0.f) continue;
-            const float4 o = *reinterpret_cast<const float4 *>(part_o + ((int64_t)s * rows + row) * kD + 4 * d4);
-            acc.x += wgt * o.x;
-            acc.y += wgt * o.y;
-            acc.z += wgt * o.z;
-            acc.w += wgt * o.w;
+    int s = 0;
+    for (; s + 4 <= num_splits; s += 4) {
+        float ls[4];
+        float4 o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            ls[j] = part_lse[(int64_t)(s + j) * rows + row];
+            o[j] = *reinterpret_cast<const float4 *>(part_o + ((int64_t)(s + j) * rows + row) * kD + 4 * d4);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float wgt = exp2_fast((ls[j] - mu) * kLog2e);
+            acc.x = fmaf(wgt, o[j].x, acc.x);
+            acc.y = fmaf(wgt, o[j].y, acc.y);
+            acc.z = fmaf(wgt, o[j].z, acc.z);
+            acc.w = fmaf(wgt, o[j].w, acc.w);
             wsum += wgt;
         }
+    }
+    for (; s < num_splits; ++s) {
+        const float wgt = exp2_fast((part_lse[(int64_t)s * rows + row] - mu) * kLog2e);
+        const float4 o = *reinterpret_cast<const float4 *>(part_o + ((int64_t)s * rows + row) * kD + 4 * d4);
+        acc.x = fmaf(wgt, o.x, acc.x);
+        acc.y = fmaf(wgt, o.y, acc.y);
+        acc.z = fmaf(wgt, o.z, acc.z);
+        acc.w = fmaf(wgt, o.w, acc.w);
+        wsum += wgt;
     }
     const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
     *reinterpret_cast<float4 *>(out + row * kD + 4 * d4) =
@@ -385,8 +433,12 @@ int make_plan(int64_t batch, int64_t max_q_len, int64_t num_heads, int64_t kv_he
         if (s > max_s) s = max_s;
         if (s < 1) s = 1;
     }
-    int64_t split_len = ceil_div(ceil_div(kv_cap > 0 ? kv_cap : 1, s), kTileN) * kTileN;
-    s = ceil_div(kv_cap > 0 ? kv_cap : 1, split_len);
+    const int64_t cap = kv_cap > 0 ? kv_cap : 1;
+    const int64_t min_s = ceil_div(cap, (int64_t)kMaxSplitPages * kPage);
+    if (s < min_s) s = min_s;
+    // splits start on page boundaries and hold at most kMaxSplitPages pages
+    int64_t split_len = ceil_div(ceil_div(cap, s), kPage) * kPage;
+    s = ceil_div(cap, split_len);
     p->splits = s;
     p->split_len = split_len;
     p->ws_bytes = s > 1 ? s * batch * max_q_len * num_heads * (kD + 1) * (int64_t)sizeof(float) : 0;
@@ -475,7 +527,14 @@ extern "C" int ck_fa_fp32_stage1(const void *q, const void *k, const void *v, co
     const int64_t grid = batch * kv_heads * p.mtiles * p.splits;
     if (grid <= 0 || grid > 0x7FFFFFFF) return CK_E_INVALID_ARG;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(stage1_kernel, dim3((unsigned)grid), dim3(kThreads), 0, s, a);
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&stage1_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+        if (e != hipSuccess) return static_cast<int>(e);
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(stage1_kernel, dim3((unsigned)grid), dim3(kThreads), kLdsBytes, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
     if (p.splits > 1) {
