@@ -54,12 +54,42 @@ __device__ __forceinline__ void dma16(const void *g, CK_LDS void *lds_base) {
                  : "memory", "m0");
 }
 
+// 4-byte global -> LDS DMA (global_load_lds_dword): lane l's word lands at
+// lds_base + 4 * l.
+__device__ __forceinline__ void dma4(const void *g, CK_LDS void *lds_base) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_base);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
+                 :
+                 : "s"(m0), "v"(g)
+                 : "memory", "m0");
+}
+
 // Wait until at most N vector-memory operations of this wave are outstanding
 // (gfx9 s_waitcnt encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4]).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Same with a wave-uniform count known only at run time. A count above the
+// largest case waits for fewer outstanding operations, which is stricter.
+__device__ __forceinline__ void wait_vmcnt_dyn(int n) {
+#define CK_WAIT_CASE(N) \
+    case N:             \
+        wait_vmcnt<N>(); \
+        break;
+    switch (n) {
+        CK_WAIT_CASE(0) CK_WAIT_CASE(1) CK_WAIT_CASE(2) CK_WAIT_CASE(3) CK_WAIT_CASE(4) CK_WAIT_CASE(5)
+        CK_WAIT_CASE(6) CK_WAIT_CASE(7) CK_WAIT_CASE(8) CK_WAIT_CASE(9) CK_WAIT_CASE(10) CK_WAIT_CASE(11)
+        CK_WAIT_CASE(12) CK_WAIT_CASE(13) CK_WAIT_CASE(14) CK_WAIT_CASE(15) CK_WAIT_CASE(16)
+        CK_WAIT_CASE(17) CK_WAIT_CASE(18) CK_WAIT_CASE(19) CK_WAIT_CASE(20)
+        default:
+            if (n < 0) wait_vmcnt<0>();
+            else wait_vmcnt<20>();
+            break;
+    }
+#undef CK_WAIT_CASE
 }
 
 // LDS transpose read (gfx950 ds_read_b64_tr_b16). Within each 16-lane group,

@@ -361,30 +361,36 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
         }
 }
 
-// N-way LSE merge of split partials: 32 threads per row, 4 dims each. Partials
-// are fetched four splits at a time with independent loads.
+// N-way LSE merge of split partials: 32 threads per row, 4 dims each. One
+// pass with an online maximum; the partials of 8 splits are fetched with
+// independent loads per round so the round trips overlap.
 __global__ __launch_bounds__(256) void stage1_combine_kernel(const float *part_o, const float *part_lse,
                                                              int num_splits, int64_t rows,
                                                              float *out, float *lse) {
+    constexpr int kBatch = 8;
     const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
     const int d4 = threadIdx.x & 31;
     if (row >= rows) return;
-    float m = -INFINITY;
-    for (int s = 0; s < num_splits; ++s) m = fmaxf(m, part_lse[(int64_t)s * rows + row]);
-    const float mu = m == -INFINITY ? 0.f : m;
+    float m = -INFINITY, wsum = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    float wsum = 0.f;
-    int s = 0;
-    for (; s + 4 <= num_splits; s += 4) {
-        float ls[4];
-        float4 o[4];
+    for (int s0 = 0; s0 < num_splits; s0 += kBatch) {
+        float ls[kBatch];
+        float4 o[kBatch];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            ls[j] = part_lse[(int64_t)(s + j) * rows + row];
-            o[j] = *reinterpret_cast<const float4 *>(part_o + ((int64_t)(s + j) * rows + row) * kD + 4 * d4);
+        for (int j = 0; j < kBatch; ++j) {
+            const int s = s0 + j < num_splits ? s0 + j : num_splits - 1;
+            ls[j] = s0 + j < num_splits ? part_lse[(int64_t)s * rows + row] : -INFINITY;
+            o[j] = *reinterpret_cast<const float4 *>(part_o + ((int64_t)s * rows + row) * kD + 4 * d4);
         }
+        float mb = m;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, ls[j]);
+        const float mu = mb == -INFINITY ? 0.f : mb;
+        const float r = exp2_fast((m - mu) * kLog2e);  // 0 while nothing has been seen
+        acc.x *= r; acc.y *= r; acc.z *= r; acc.w *= r;
+        wsum *= r;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
             const float wgt = exp2_fast((ls[j] - mu) * kLog2e);
             acc.x = fmaf(wgt, o[j].x, acc.x);
             acc.y = fmaf(wgt, o[j].y, acc.y);
@@ -392,15 +398,7 @@ __global__ __launch_bounds__(256) void stage1_combine_kernel(const float *part_o
             acc.w = fmaf(wgt, o[j].w, acc.w);
             wsum += wgt;
         }
-    }
-    for (; s < num_splits; ++s) {
-        const float wgt = exp2_fast((part_lse[(int64_t)s * rows + row] - mu) * kLog2e);
-        const float4 o = *reinterpret_cast<const float4 *>(part_o + ((int64_t)s * rows + row) * kD + 4 * d4);
-        acc.x = fmaf(wgt, o.x, acc.x);
-        acc.y = fmaf(wgt, o.y, acc.y);
-        acc.z = fmaf(wgt, o.z, acc.z);
-        acc.w = fmaf(wgt, o.w, acc.w);
-        wsum += wgt;
+        m = mb;
     }
     const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
     *reinterpret_cast<float4 *>(out + row * kD + 4 * d4) =

@@ -11,23 +11,32 @@
 // fp32 P and fp32 accumulation (no bf16 rounding of P: there is no matrix
 // core here to feed), O = acc / l, LSE = ln(l) + max.
 //
-// MI355X design: memory-bound streaming with a persistent, token-balanced grid.
+// MI355X design: memory-bound streaming with a persistent, balanced grid.
 // * Suffix lengths vary widely (geometric in the benchmark), and a workgroup
 //   pays several microseconds of start-up (lengths, page ids, first DMA round
-//   trip) before its first byte of K/V. So instead of one workgroup per
-//   (sequence, split), workgroup (kv head g, chunk c) takes the c-th 1/P of the
-//   concatenation of all sequences' tokens for head g, crossing sequence
-//   boundaries; every workgroup moves the same number of bytes and starts once.
-//   Prefix sums of the (device-side) lengths are computed per workgroup in LDS.
-// * K and V rows stream through a 4-stage LDS ring (64 tokens = 32 KB per
-//   stage) by global->LDS DMA, continuously across sequence boundaries; a
-//   sequence's q rows ride along with its first stage. Page ids are fetched
-//   with scalar loads (lgkmcnt), so looking one up never drains the DMA ring.
-// * Each of the 8 waves (2 per SIMD) consumes 8 tokens of a stage as 4 token
-//   slots x 16 lanes x 8 dims; q.k uses the packed bf16 dot product
-//   (v_dot2_f32_bf16), the 16-lane sum uses DPP row rotations, V is unpacked
-//   once per token for all query heads of the group. At the end of a sequence
-//   segment the slots merge with two xor-shuffles and the 8 waves through the
+//   trip) before its first byte of K/V. So the work is cut into windows of 64
+//   tokens of one sequence (the last window of a sequence may be short), and
+//   workgroup (kv head g, chunk c) takes the c-th 1/P of the list of all
+//   windows, crossing sequence boundaries: every workgroup streams the same
+//   number of windows and starts once. Window and length prefix sums are built
+//   per workgroup in LDS from the device-side lengths.
+// * K and V rows stream through a 4-stage LDS ring (one window, 32 KB, per
+//   stage) by global->LDS DMA, continuously across sequence boundaries. A
+//   stage's DMA group also carries the block-table entry of the stage three
+//   ahead (so page ids never wait on memory inside the loop) and, on the first
+//   window of a sequence, its q rows. Each wave counts its own vector-memory
+//   operations (DMAs and output stores) and waits for exactly one stage. Half
+//   the waves issue the next group right after the stage barrier and half after
+//   their compute, so the DMA issue of one half overlaps the other's arithmetic.
+// * Scores: lane (t, c) of wave w holds token 8w + t, dims 8c..8c+7 and
+//   64+8c..64+8c+7; q.k is eight packed bf16 dot products (v_dot2_f32_bf16,
+//   two chains) and a 3-step DPP sum over the token's 8 lanes.
+// * Softmax: the running max is uniform over the wave and moves only when a
+//   score exceeds it by more than 2^kTau (a wave-uniform branch), so rescaling
+//   is rare; any reference point gives the same O and LSE.
+// * Values: lane l accumulates dims 2l, 2l+1 of every query head over all of
+//   the wave's tokens; the token weights reach the lanes as LDS broadcasts.
+//   Closing a sequence therefore needs only a cross-wave merge through the
 //   just-consumed ring stage.
 // * A segment that is a whole sequence writes bf16 O and the LSE directly; a
 //   sequence cut by a chunk boundary leaves fp32 partials that a small fix-up
@@ -41,15 +50,26 @@ constexpr int kD = 128;
 constexpr int kPage = 128;
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
-constexpr int kStageTokens = 64;
+constexpr int kWin = 64;                           // tokens per window (= per ring stage)
 constexpr int kStages = 4;
-constexpr int kTileBytes = kStageTokens * kD * 2;  // 16 KB of K (and of V) per stage
+constexpr int kTileBytes = kWin * kD * 2;          // 16 KB of K (and of V) per stage
 constexpr int kMaxGroup = 8;
 constexpr int kQBytes = kMaxGroup * kD * 2;        // q rows of one (sequence, kv head)
 constexpr int kStageBytes = 2 * kTileBytes + kQBytes;
 constexpr int kMaxBatch = 2048;                    // sequences per launch (prefix sums in LDS)
-constexpr int kDmaPerStage = 2 * (kTileBytes / 1024) / kWaves;  // K/V DMAs per wave per stage (4)
-constexpr int kLdsBytes = kStages * kStageBytes + (kMaxBatch + 1 + 15) * 4 + 64;
+constexpr int kPgRing = 8;                         // block-table entries in flight
+constexpr int kKvDmaPerWave = 2 * (kTileBytes / 1024) / kWaves;  // 4
+constexpr float kTau = 8.0f;                       // log2 headroom before the running max moves
+
+// LDS layout (bytes)
+constexpr int kCwOff = kStages * kStageBytes;                 // int cw[kMaxBatch + 1]: window prefix sums
+constexpr int kLenOff = kCwOff + ((kMaxBatch + 1) * 4 + 15) / 16 * 16;  // int len[kMaxBatch]
+constexpr int kWtotOff = kLenOff + kMaxBatch * 4;             // int wtot[kWaves] scan scratch
+constexpr int kPgOff = kWtotOff + kWaves * 4;                 // int pgring[kPgRing]
+constexpr int kPwOff = kPgOff + kPgRing * 4;                  // float pw[kWaves][8][kMaxGroup]
+constexpr int kLdsBytes = kPwOff + kWaves * 8 * kMaxGroup * 4;
+static_assert(kPwOff % 16 == 0, "p broadcast rows are read 16 bytes at a time");
+static_assert(kLdsBytes <= 160 * 1024, "fits the CU's LDS");
 
 struct SuffixArgs {
     const uint16_t *q;
@@ -61,7 +81,7 @@ struct SuffixArgs {
     float *lse;
     float *part_o;    // [kv_heads][chunks][2][G][kD]
     float *part_lse;  // [kv_heads][chunks][2][G]
-    int32_t *cu_out;  // [batch + 1] prefix sums, written by workgroup 0
+    int32_t *cw_out;  // [batch + 1] window prefix sums, written by workgroup 0
     int64_t bt_cols;
     int64_t num_blocks;
     int batch;
@@ -73,41 +93,32 @@ struct SuffixArgs {
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-// Sum over the 16 lanes of a DPP row; every lane of the row receives the total.
-__device__ __forceinline__ float row16_sum(float x) {
-    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xF, 0xF, false));  // row_ror:8
-    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x124, 0xF, 0xF, false));  // row_ror:4
-    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x122, 0xF, 0xF, false));  // row_ror:2
-    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x121, 0xF, 0xF, false));  // row_ror:1
+#define CK_DPP(x, ctrl) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), ctrl, 0xF, 0xF, false))
+
+// Sum over each aligned group of 8 lanes; every lane of the group gets the total.
+__device__ __forceinline__ float sum8(float x) {
+    x += CK_DPP(x, 0xB1);   // quad_perm [1,0,3,2]
+    x += CK_DPP(x, 0x4E);   // quad_perm [2,3,0,1]
+    x += CK_DPP(x, 0x141);  // row_half_mirror: the other quad of the 8
     return x;
+}
+// Reduce a value that is constant within each 8-lane group over the 8 groups.
+__device__ __forceinline__ float max_groups(float x) {
+    x = fmaxf(x, CK_DPP(x, 0x128));  // row_ror:8, the other group of the 16-lane row
+    x = fmaxf(x, __shfl_xor(x, 16));
+    return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ __forceinline__ float sum_groups(float x) {
+    x += CK_DPP(x, 0x128);
+    x += __shfl_xor(x, 16);
+    return x + __shfl_xor(x, 32);
 }
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
                                            false);
-}
-
-// q.k over this lane's 8 dims (4 packed bf16 pairs each), fp32 accumulate.
-__device__ __forceinline__ float dot8(const uint4 &k, const uint4 &q) {
-    float d = dot2(k.x, q.x, 0.f);
-    d = dot2(k.y, q.y, d);
-    d = dot2(k.z, q.z, d);
-    return dot2(k.w, q.w, d);
-}
-
-// Scalar (SMEM) load of one int: waits on lgkmcnt only, never on the vector
-// memory counter the DMA ring uses.
-__device__ __forceinline__ int sload_i32(const int32_t *p) {
-    int v;
-    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
-    return v;
-}
-
-__device__ __forceinline__ void wait_stages(int outstanding) {
-    if (outstanding >= 2) wait_vmcnt<2 * kDmaPerStage>();
-    else if (outstanding == 1) wait_vmcnt<kDmaPerStage>();
-    else wait_vmcnt<0>();
 }
 
 __device__ __forceinline__ int64_t clamp_len(const SuffixArgs &a, int64_t kvl) {
@@ -118,60 +129,66 @@ __device__ __forceinline__ int64_t clamp_len(const SuffixArgs &a, int64_t kvl) {
     return kvl < 0 ? 0 : kvl;
 }
 
-// Walk over the stages of a workgroup's token range [r0, r1): a stage is a
-// 64-token aligned window of one sequence; consecutive stages cross sequences.
+// Walk over the windows of a workgroup's window range [w0, w1) of the list of
+// all windows; consecutive windows cross sequences. Values are wave-uniform.
 struct Cursor {
-    int b;      // sequence
-    int jst;    // sequence-local first token of the stage window (multiple of 64)
-    int sj0;    // sequence-local start of this workgroup's segment of b
-    int sj1;    // sequence-local end of the segment
+    int b;       // sequence
+    int k;       // window index inside the sequence (tokens 64k ..)
+    int kfirst;  // first window of this workgroup's segment of b
+    int kend;    // one past the segment's last window
     bool valid;
 };
 
-__device__ __forceinline__ void cursor_seg(Cursor &cur, const CK_LDS int *cu, int64_t r0, int64_t r1) {
-    const int base = cu[cur.b];
-    cur.sj0 = (int)((r0 > base ? r0 : base) - base);
-    const int64_t e = cu[cur.b + 1];
-    cur.sj1 = (int)((r1 < e ? r1 : e) - base);
-    cur.jst = (cur.sj0 / kStageTokens) * kStageTokens;
+__device__ __forceinline__ void cursor_seg(Cursor &cur, const CK_LDS int *cw, int w0, int w1) {
+    const int base = cw[cur.b];
+    cur.k = (w0 > base ? w0 : base) - base;
+    const int e = cw[cur.b + 1];
+    cur.kend = (w1 < e ? w1 : e) - base;
+    cur.kfirst = cur.k;
 }
 
-__device__ __forceinline__ void cursor_next(Cursor &cur, const CK_LDS int *cu, int batch, int64_t r0, int64_t r1) {
-    cur.jst += kStageTokens;
-    if (cur.jst < cur.sj1) return;
+__device__ __forceinline__ void cursor_next(Cursor &cur, const CK_LDS int *cw, int batch, int w0, int w1) {
+    if (!cur.valid) return;
+    if (++cur.k < cur.kend) return;
     int b = cur.b + 1;
-    while (b < batch && cu[b + 1] == cu[b]) ++b;  // empty sequences have no stages
-    if (b >= batch || cu[b] >= r1) {
+    while (b < batch && cw[b + 1] == cw[b]) ++b;  // empty sequences have no windows
+    if (b >= batch || cw[b] >= w1) {
         cur.valid = false;
         return;
     }
     cur.b = b;
-    cursor_seg(cur, cu, r0, r1);
+    cursor_seg(cur, cw, w0, w1);
 }
 
 template <int G>
 __global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
     CK_LDS char *smem = (CK_LDS char *)smem_raw;
-    CK_LDS int *cu = (CK_LDS int *)(smem + kStages * kStageBytes);  // [batch + 1]
-    CK_LDS int *wtot = cu + kMaxBatch + 1;                            // [kWaves] scan scratch
-    CK_LDS int *slot_ok = wtot + kWaves;                              // [kStages] page validity
+    CK_LDS int *cw = (CK_LDS int *)(smem + kCwOff);
+    CK_LDS int *len = (CK_LDS int *)(smem + kLenOff);
+    CK_LDS int *wtot = (CK_LDS int *)(smem + kWtotOff);
+    CK_LDS int *pgring = (CK_LDS int *)(smem + kPgOff);
+    constexpr int kPwRow = (G + 3) / 4 * 4;  // floats per token in the broadcast rows
+    constexpr int kQWaves = (G * 16 + 63) / 64;  // waves whose lanes carry the q rows
 
     const int tid = threadIdx.x;
-    const int wid = tid >> 6;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
-    const int slot = lane >> 4;
-    const int c = lane & 15;
+    const int t = lane >> 3;  // token slot of this lane in the wave's 8 tokens
+    const int c = lane & 7;   // column pair: dims 8c.. and 64+8c..
     const int g = blockIdx.x % a.kv_heads;
     const int chunk = blockIdx.x / a.kv_heads;
+    CK_LDS float *pw = (CK_LDS float *)(smem + kPwOff) + wid * 8 * kPwRow;
 
-    // ---- prefix sums of the clamped lengths (4 per thread, block scan) ------------
+    // ---- lengths and window prefix sums (4 sequences per thread, block scan) ------
     int lv[4];
     int local = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int i = 4 * tid + j;
-        lv[j] = i < a.batch ? (int)clamp_len(a, a.kv_seqlens[i]) : 0;
+        const int ln = i < a.batch ? (int)clamp_len(a, a.kv_seqlens[i]) : 0;
+        if (i < a.batch) len[i] = ln;
+        lv[j] = (ln + kWin - 1) / kWin;
         local += lv[j];
     }
     int x = local;
@@ -189,238 +206,266 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
     for (int j = 0; j < 4; ++j) {
         const int i = 4 * tid + j;
         run += lv[j];
-        if (i < a.batch) cu[i + 1] = run;
+        if (i < a.batch) cw[i + 1] = run;
     }
-    if (tid == 0) cu[0] = 0;
+    if (tid == 0) cw[0] = 0;
     __syncthreads();
     if (blockIdx.x == 0)
-        for (int i = tid; i <= a.batch; i += kThreads) a.cu_out[i] = cu[i];
+        for (int i = tid; i <= a.batch; i += kThreads) a.cw_out[i] = cw[i];
 
-    const int64_t T = cu[a.batch];
-    const int64_t r0 = (int64_t)chunk * T / a.chunks;
-    const int64_t r1 = (int64_t)(chunk + 1) * T / a.chunks;
-    if (r0 >= r1) return;  // uniform over the workgroup
+    const int W = cw[a.batch];
+    const int w0 = (int)((int64_t)chunk * W / a.chunks);
+    const int w1 = (int)((int64_t)(chunk + 1) * W / a.chunks);
+    if (w0 >= w1) return;  // uniform over the workgroup
 
-    // first sequence: largest b with cu[b] <= r0 (then cu[b + 1] > r0)
+    // first sequence: largest b with cw[b] <= w0 (then cw[b + 1] > w0)
     int lo = 0, hi = a.batch;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (cu[mid] <= r0) lo = mid;
+        if (cw[mid] <= w0) lo = mid;
         else hi = mid - 1;
     }
-    Cursor ic;
-    ic.b = lo;
-    ic.valid = true;
-    cursor_seg(ic, cu, r0, r1);
-    Cursor cc = ic;
+    Cursor cc;
+    cc.b = lo;
+    cc.valid = true;
+    cursor_seg(cc, cw, w0, w1);
+
+    // page ids of the first kStages - 1 windows; later ones travel with the ring
+    Cursor pc = cc;
+    for (int j = 0; j < kStages - 1; ++j) {
+        if (pc.valid && tid == j) pgring[j] = a.bt[(int64_t)pc.b * a.bt_cols + pc.k * kWin / kPage];
+        cursor_next(pc, cw, a.batch, w0, w1);
+    }
+    __syncthreads();
 
     const int64_t head_stride = (int64_t)a.kv_heads * kD;
-    auto issue = [&](const Cursor &cur, int n) {
+    int tot = 0;  // vector-memory operations this wave has issued (wave-uniform)
+    // DMA group of window n (cursor cur): the block-table entry of window n + 3
+    // (cursor pcur; wave 0), the window's K and V rows, and on the first window
+    // of a segment the sequence's q rows.
+    auto issue = [&](const Cursor &cur, const Cursor &pcur, int n) {
         CK_LDS char *kb = smem + (n % kStages) * kStageBytes;
         CK_LDS char *vb = kb + kTileBytes;
         CK_LDS char *qb = vb + kTileBytes;
-        int page = sload_i32(a.bt + (int64_t)cur.b * a.bt_cols + cur.jst / kPage);
-        const bool ok = page >= 0 && (int64_t)page < a.num_blocks;
-        if (tid == 0) slot_ok[n % kStages] = ok ? 1 : 0;
-        if (!ok) page = 0;  // keep the per-wave DMA count exact; rows are zeroed at use
-        const int64_t tok0 = (int64_t)page * kPage + (cur.jst % kPage);
+        if (wid == 0) {
+            const int32_t *psrc = pcur.valid ? a.bt + (int64_t)pcur.b * a.bt_cols + pcur.k * kWin / kPage : a.bt;
+            if (lane == 0) dma4(psrc, pgring + (n + kStages - 1) % kPgRing);
+            ++tot;
+        }
+        int page = pgring[n % kPgRing];
+        if (page < 0 || (int64_t)page >= a.num_blocks) page = 0;  // rows ignored at use
+        const int64_t tok0 = (int64_t)page * kPage + (cur.k * kWin) % kPage;
 #pragma unroll
-        for (int j = 0; j < kDmaPerStage / 2; ++j) {
-            const int blk = wid * (kDmaPerStage / 2) + j;  // 4 token rows per DMA
-            const int tt = blk * 4 + (lane >> 4);
-            const int64_t off = (tok0 + tt) * head_stride + g * kD + (lane & 15) * 8;
+        for (int j = 0; j < kKvDmaPerWave / 2; ++j) {
+            const int blk = wid * (kKvDmaPerWave / 2) + j;  // 4 token rows per DMA
+            const int64_t off = (tok0 + blk * 4 + (lane >> 4)) * head_stride + g * kD + (lane & 15) * 8;
             dma16(a.k + off, kb + blk * 1024);
             dma16(a.v + off, vb + blk * 1024);
         }
-        // the sequence's q rows (G x 256 B, contiguous) with its first stage
-        if (cur.jst == (cur.sj0 / kStageTokens) * kStageTokens && wid * 64 < G * 16) {
-            if (lane < G * 16 - wid * 64)
+        tot += kKvDmaPerWave;
+        if (cur.k == cur.kfirst && wid < kQWaves) {
+            if (wid * 64 + lane < G * 16)
                 dma16(a.q + ((int64_t)cur.b * a.num_heads + g * G) * kD + (wid * 64 + lane) * 8, qb + wid * 1024);
+            ++tot;
         }
     };
 
-    int n_issued = 0;
-    for (int k = 0; k < kStages - 1 && ic.valid; ++k) {
-        issue(ic, n_issued++);
-        cursor_next(ic, cu, a.batch, r0, r1);
+    // tot right after issuing each group still in flight (oldest first)
+    int gend0 = 0, gend1 = 0, gend2 = 0;
+    Cursor ic = cc;
+    for (int j = 0; j < kStages - 1; ++j) {
+        if (ic.valid) issue(ic, pc, j);
+        gend0 = gend1;
+        gend1 = gend2;
+        gend2 = tot;
+        cursor_next(ic, cw, a.batch, w0, w1);
+        cursor_next(pc, cw, a.batch, w0, w1);
     }
+    // after the prologue gend0..2 hold groups 0..2
 
-    uint4 qp[G];
-    float m[G], l[G], acc[G][8];
+    uint32_t qr[G][8];
+    float m[G], thr[G], l[G], acc[G][2];
     int n_done = 0;
     while (cc.valid) {
-        wait_stages(n_issued - n_done - 1);
+        // everything issued after this window's group may stay in flight
+        wait_vmcnt_dyn(__builtin_amdgcn_readfirstlane(tot - gend0));
         __syncthreads();
         const int st = n_done % kStages;
+        // the next group goes into the stage consumed last iteration; half the
+        // waves issue before computing and half after, so the address unit
+        // drains one half's DMAs while the other half computes
+        const bool early = wid < kWaves / 2;
+        if (early && ic.valid) issue(ic, pc, n_done + kStages - 1);
+
         CK_LDS char *kb = smem + st * kStageBytes;
         CK_LDS char *vb = kb + kTileBytes;
         CK_LDS char *qb = vb + kTileBytes;
-        const int tlo = (cc.sj0 > cc.jst ? cc.sj0 : cc.jst) - cc.jst;
-        const int thi = (cc.sj1 < cc.jst + kStageTokens ? cc.sj1 : cc.jst + kStageTokens) - cc.jst;
-        const bool first = cc.jst == (cc.sj0 / kStageTokens) * kStageTokens;
-        const bool last = cc.jst + kStageTokens >= cc.sj1;
-        const bool page_ok = slot_ok[st] != 0;
-        if (tlo > 0 || thi < kStageTokens || !page_ok) {
-            // rows outside this segment (or of an invalid page) may hold anything:
-            // zero them so 0 * V cannot produce a NaN
-            for (int idx = tid; idx < kStageTokens * 16; idx += kThreads) {
-                const int tt = idx >> 4, cc16 = idx & 15;
-                if (!page_ok || tt < tlo || tt >= thi) {
-                    *reinterpret_cast<CK_LDS u32x4 *>(kb + tt * 256 + cc16 * 16) = u32x4{0, 0, 0, 0};
-                    *reinterpret_cast<CK_LDS u32x4 *>(vb + tt * 256 + cc16 * 16) = u32x4{0, 0, 0, 0};
-                }
-            }
-            __syncthreads();
-        }
-        if (ic.valid) {
-            issue(ic, n_issued++);
-            cursor_next(ic, cu, a.batch, r0, r1);
-        }
+        const int b = cc.b;
+        const int thi = min(kWin, len[b] - cc.k * kWin);  // tokens of this window
+        const bool first = cc.k == cc.kfirst;
+        const bool last = cc.k + 1 == cc.kend;
+        const int praw = pgring[n_done % kPgRing];
+        const bool page_ok = praw >= 0 && (int64_t)praw < a.num_blocks;
         if (first) {
 #pragma unroll
-            for (int hq = 0; hq < G; ++hq) {
-                const u32x4 qq = *reinterpret_cast<const CK_LDS u32x4 *>(qb + hq * 256 + c * 16);
-                const uint32_t q0 = qq[0], q1 = qq[1], q2 = qq[2], q3 = qq[3];
-                qp[hq] = make_uint4(q0, q1, q2, q3);
-                m[hq] = -INFINITY;
-                l[hq] = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[hq][e] = 0.f;
+            for (int h = 0; h < G; ++h) {
+                const u32x4 q0 = *reinterpret_cast<const CK_LDS u32x4 *>(qb + h * 256 + c * 16);
+                const u32x4 q1 = *reinterpret_cast<const CK_LDS u32x4 *>(qb + h * 256 + 128 + c * 16);
+                qr[h][0] = q0[0]; qr[h][1] = q0[1]; qr[h][2] = q0[2]; qr[h][3] = q0[3];
+                qr[h][4] = q1[0]; qr[h][5] = q1[1]; qr[h][6] = q1[2]; qr[h][7] = q1[3];
+                m[h] = -INFINITY;
+                thr[h] = -INFINITY;
+                l[h] = 0.f;
+                acc[h][0] = 0.f;
+                acc[h][1] = 0.f;
             }
         }
 
-        // this wave: tokens 8*wid + 4u + slot, u = 0..1
-        const int tbase = 8 * wid;
-        if (tbase < thi && tbase + 8 > tlo) {
-            uint4 kr[2];
-            float vf[2][8];
+        // this wave's tokens 8 * wid + [0, t1)
+        const int t1 = min(8, thi - 8 * wid);
+        if (t1 > 0) {
+            const int tt = 8 * wid + t;
+            const u32x4 k0 = *reinterpret_cast<const CK_LDS u32x4 *>(kb + tt * 256 + c * 16);
+            const u32x4 k1 = *reinterpret_cast<const CK_LDS u32x4 *>(kb + tt * 256 + 128 + c * 16);
+            const uint32_t kr[8] = {k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
+            const bool tok_ok = t < t1;
+            float s[G];
+            bool trig = false;
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int tt = tbase + 4 * u + slot;
-                const u32x4 kk = *reinterpret_cast<const CK_LDS u32x4 *>(kb + tt * 256 + c * 16);
-                const u32x4 vv = *reinterpret_cast<const CK_LDS u32x4 *>(vb + tt * 256 + c * 16);
-                const uint32_t k0 = kk[0], k1 = kk[1], k2 = kk[2], k3 = kk[3];
-                const uint32_t v0 = vv[0], v1 = vv[1], v2 = vv[2], v3 = vv[3];
-                kr[u] = make_uint4(k0, k1, k2, k3);
-                vf[u][0] = bf16_lo(v0); vf[u][1] = bf16_hi(v0);
-                vf[u][2] = bf16_lo(v1); vf[u][3] = bf16_hi(v1);
-                vf[u][4] = bf16_lo(v2); vf[u][5] = bf16_hi(v2);
-                vf[u][6] = bf16_lo(v3); vf[u][7] = bf16_hi(v3);
+            for (int h = 0; h < G; ++h) {
+                float d0 = dot2(kr[0], qr[h][0], 0.f);
+                float d1 = dot2(kr[4], qr[h][4], 0.f);
+#pragma unroll
+                for (int e = 1; e < 4; ++e) {
+                    d0 = dot2(kr[e], qr[h][e], d0);
+                    d1 = dot2(kr[4 + e], qr[h][4 + e], d1);
+                }
+                float d = sum8(d0 + d1);
+                d = page_ok ? d : 0.f;  // an invalid page reads as zero rows
+                s[h] = tok_ok ? d * a.scale_log2 : -INFINITY;
+                trig |= s[h] > thr[h];
             }
+            if (__builtin_amdgcn_ballot_w64(trig)) {
+                // some score passed its head's headroom: move the reference maxima
 #pragma unroll
-            for (int hq = 0; hq < G; ++hq) {
-                float s[2];
-                float smax = -INFINITY;
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const int tt = tbase + 4 * u + slot;
-                    const float d = row16_sum(dot8(kr[u], qp[hq])) * a.scale_log2;
-                    s[u] = (tt >= tlo && tt < thi) ? d : -INFINITY;
-                    smax = fmaxf(smax, s[u]);
+                for (int h = 0; h < G; ++h) {
+                    const float m_new = fmaxf(m[h], max_groups(s[h]));
+                    if (m_new > m[h]) {
+                        const float f = exp2_fast(m[h] - m_new);  // 0 from -inf
+                        acc[h][0] *= f;
+                        acc[h][1] *= f;
+                        l[h] *= f;
+                        m[h] = m_new;
+                        thr[h] = m_new + kTau;
+                    }
                 }
-                const float m_new = fmaxf(m[hq], smax);
-                const float m_use = m_new == -INFINITY ? 0.f : m_new;
-                const float dm = exp2_fast(m[hq] - m_use);
-                float ps = 0.f;
+            }
+            float p[kPwRow];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[hq][e] *= dm;
+            for (int h = 0; h < kPwRow; ++h) p[h] = 0.f;
 #pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const float p = exp2_fast(s[u] - m_use);
-                    ps += p;
+            for (int h = 0; h < G; ++h) {
+                p[h] = exp2_fast(s[h] - (m[h] == -INFINITY ? 0.f : m[h]));  // 0 for masked tokens
+                l[h] += p[h];
+            }
+            if (c == 0) {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[hq][e] = fmaf(p, vf[u][e], acc[hq][e]);
+                for (int h4 = 0; h4 < kPwRow; h4 += 4)
+                    *reinterpret_cast<CK_LDS f32x4 *>(pw + t * kPwRow + h4) =
+                        f32x4{p[h4], p[h4 + 1], p[h4 + 2], p[h4 + 3]};
+            }
+            if (page_ok) {
+                // acc[h][dims 2*lane, 2*lane + 1] += p[token][h] * V[token]
+                auto pv_token = [&](int j) {
+                    const uint32_t vv =
+                        *reinterpret_cast<const CK_LDS uint32_t *>(vb + (8 * wid + j) * 256 + lane * 4);
+                    const float v0 = bf16_lo(vv), v1 = bf16_hi(vv);
+#pragma unroll
+                    for (int h4 = 0; h4 < kPwRow; h4 += 4) {
+                        const f32x4 pv = *reinterpret_cast<const CK_LDS f32x4 *>(pw + j * kPwRow + h4);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            if (h4 + e < G) {
+                                acc[h4 + e][0] = fmaf(pv[e], v0, acc[h4 + e][0]);
+                                acc[h4 + e][1] = fmaf(pv[e], v1, acc[h4 + e][1]);
+                            }
+                        }
+                    }
+                };
+                if (t1 == 8) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) pv_token(j);
+                } else {
+                    for (int j = 0; j < t1; ++j) pv_token(j);
                 }
-                l[hq] = l[hq] * dm + ps;
-                m[hq] = m_new;
             }
         }
+
+        if (!early && ic.valid) issue(ic, pc, n_done + kStages - 1);
+        gend0 = gend1;
+        gend1 = gend2;
+        gend2 = tot;
+        cursor_next(ic, cw, a.batch, w0, w1);
+        cursor_next(pc, cw, a.batch, w0, w1);
 
         if (last) {
-            // ---- finalize the segment: 4 slots (shuffles) then 8 waves (LDS) ----
+            // ---- close the segment: per-wave sums, then the 8 waves through LDS ----
 #pragma unroll
-            for (int off = 16; off <= 32; off <<= 1) {
+            for (int h = 0; h < G; ++h) l[h] = sum_groups(l[h]);  // token-slot partials
+            __syncthreads();  // every wave is done with this stage (q is in registers)
+            CK_LDS float *xacc = (CK_LDS float *)kb;    // [kWaves][G][kD]
+            CK_LDS float *xm = xacc + kWaves * G * kD;  // [kWaves][G]
+            CK_LDS float *xl = xm + kWaves * G;         // [kWaves][G]
 #pragma unroll
-                for (int hq = 0; hq < G; ++hq) {
-                    const float mo = __shfl_xor(m[hq], off);
-                    const float lo2 = __shfl_xor(l[hq], off);
-                    const float mn = fmaxf(m[hq], mo);
-                    const float mu = mn == -INFINITY ? 0.f : mn;
-                    const float fa = exp2_fast(m[hq] - mu), fb = exp2_fast(mo - mu);
+            for (int h = 0; h < G; ++h)
+                *reinterpret_cast<CK_LDS f32x2 *>(xacc + (wid * G + h) * kD + 2 * lane) = f32x2{acc[h][0], acc[h][1]};
+            if (lane == 0) {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float ao = __shfl_xor(acc[hq][e], off);
-                        acc[hq][e] = acc[hq][e] * fa + ao * fb;
-                    }
-                    l[hq] = l[hq] * fa + lo2 * fb;
-                    m[hq] = mn;
-                }
-            }
-            __syncthreads();  // every wave is done with this stage's K/V (q is in registers)
-            CK_LDS float *xacc = (CK_LDS float *)kb;            // [kWaves][G][kD], spans K, V and q areas
-            CK_LDS float *xm = xacc + kWaves * G * kD;          // [kWaves][G]
-            CK_LDS float *xl = xm + kWaves * G;                 // [kWaves][G]
-            if (slot == 0) {
-#pragma unroll
-                for (int hq = 0; hq < G; ++hq) {
-                    *reinterpret_cast<CK_LDS f32x4 *>(xacc + (wid * G + hq) * kD + 8 * c) =
-                        f32x4{acc[hq][0], acc[hq][1], acc[hq][2], acc[hq][3]};
-                    *reinterpret_cast<CK_LDS f32x4 *>(xacc + (wid * G + hq) * kD + 8 * c + 4) =
-                        f32x4{acc[hq][4], acc[hq][5], acc[hq][6], acc[hq][7]};
-                    if (c == 0) {
-                        xm[wid * G + hq] = m[hq];
-                        xl[wid * G + hq] = l[hq];
-                    }
+                for (int h = 0; h < G; ++h) {
+                    xm[wid * G + h] = m[h];
+                    xl[wid * G + h] = l[h];
                 }
             }
             __syncthreads();
-            const int b = cc.b;
-            const bool head_part = (int64_t)cu[b] < r0;
-            const bool tail_part = (int64_t)cu[b + 1] > r1;
-            for (int idx = tid; idx < G * 16; idx += kThreads) {
-                const int hq = idx >> 4, cc8 = idx & 15;
-                float mn = -INFINITY;
+            if (wid < G) {
+                const int h = wid;
+                float mx = -INFINITY;
 #pragma unroll
-                for (int ww = 0; ww < kWaves; ++ww) mn = fmaxf(mn, xm[ww * G + hq]);
-                const float mu = mn == -INFINITY ? 0.f : mn;
-                float lt = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                for (int ww = 0; ww < kWaves; ++ww) mx = fmaxf(mx, xm[ww * G + h]);
+                const float mu = mx == -INFINITY ? 0.f : mx;
+                float lt = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
                 for (int ww = 0; ww < kWaves; ++ww) {
-                    const float f = exp2_fast(xm[ww * G + hq] - mu);
-                    lt += xl[ww * G + hq] * f;
-                    const f32x4 a0 = *reinterpret_cast<const CK_LDS f32x4 *>(xacc + (ww * G + hq) * kD + 8 * cc8);
-                    const f32x4 a1 = *reinterpret_cast<const CK_LDS f32x4 *>(xacc + (ww * G + hq) * kD + 8 * cc8 + 4);
-                    o[0] += a0[0] * f; o[1] += a0[1] * f; o[2] += a0[2] * f; o[3] += a0[3] * f;
-                    o[4] += a1[0] * f; o[5] += a1[1] * f; o[6] += a1[2] * f; o[7] += a1[3] * f;
+                    const float f = exp2_fast(xm[ww * G + h] - mu);
+                    lt = fmaf(xl[ww * G + h], f, lt);
+                    const f32x2 xa = *reinterpret_cast<const CK_LDS f32x2 *>(xacc + (ww * G + h) * kD + 2 * lane);
+                    o0 = fmaf(xa[0], f, o0);
+                    o1 = fmaf(xa[1], f, o1);
                 }
                 const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-                const float lse_v = lt > 0.f ? (mn + __log2f(lt)) * kLn2 : -INFINITY;
+                const float lse_v = lt > 0.f ? (mx + __log2f(lt)) * kLn2 : -INFINITY;
+                const bool head_part = cw[b] < w0;
+                const bool tail_part = cw[b + 1] > w1;
                 if (!head_part && !tail_part) {
-                    const int64_t row = (int64_t)b * a.num_heads + g * G + hq;
-                    uint4 ow;
-                    ow.x = pack_bf16x2(o[0] * inv, o[1] * inv);
-                    ow.y = pack_bf16x2(o[2] * inv, o[3] * inv);
-                    ow.z = pack_bf16x2(o[4] * inv, o[5] * inv);
-                    ow.w = pack_bf16x2(o[6] * inv, o[7] * inv);
-                    *reinterpret_cast<uint4 *>(a.out + row * kD + 8 * cc8) = ow;
-                    if (cc8 == 0) a.lse[row] = lse_v;
+                    const int64_t row = (int64_t)b * a.num_heads + g * G + h;
+                    *reinterpret_cast<uint32_t *>(a.out + row * kD + 2 * lane) = pack_bf16x2(o0 * inv, o1 * inv);
+                    if (lane == 0) a.lse[row] = lse_v;
                 } else {
-                    const int64_t pidx = (((int64_t)g * a.chunks + chunk) * 2 + (head_part ? 0 : 1)) * G + hq;
-                    float4 *dst = reinterpret_cast<float4 *>(a.part_o + pidx * kD + 8 * cc8);
-                    dst[0] = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
-                    dst[1] = make_float4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
-                    if (cc8 == 0) a.part_lse[pidx] = lse_v;
+                    const int64_t pidx = (((int64_t)g * a.chunks + chunk) * 2 + (head_part ? 0 : 1)) * G + h;
+                    *reinterpret_cast<float2 *>(a.part_o + pidx * kD + 2 * lane) = make_float2(o0 * inv, o1 * inv);
+                    if (lane == 0) a.part_lse[pidx] = lse_v;
                 }
+                tot += 2;  // one O store and one LSE store
             }
         }
         ++n_done;
-        cursor_next(cc, cu, a.batch, r0, r1);
+        cursor_next(cc, cw, a.batch, w0, w1);
     }
 }
 
-// Chunk that owns stream position p: chunk c covers [c*T/P, (c+1)*T/P).
-__device__ __forceinline__ int owner_chunk(int64_t p, int64_t T, int P) {
-    return (int)(((p + 1) * P - 1) / T);
+// Chunk that owns window p: chunk c covers windows [c*W/P, (c+1)*W/P).
+__device__ __forceinline__ int owner_chunk(int64_t p, int64_t W, int P) {
+    return (int)(((p + 1) * P - 1) / W);
 }
 
 // One workgroup per (sequence, kv head): empty suffixes get O = 0, LSE = -inf;
@@ -432,26 +477,26 @@ __global__ __launch_bounds__(256) void suffix_fixup_kernel(SuffixArgs a) {
     const int hq = threadIdx.x >> 5;
     const int d4 = threadIdx.x & 31;
     if (hq >= G) return;
-    const int64_t beg = a.cu_out[b], end = a.cu_out[b + 1], T = a.cu_out[a.batch];
+    const int64_t beg = a.cw_out[b], end = a.cw_out[b + 1], W = a.cw_out[a.batch];
     const int64_t row = (int64_t)b * a.num_heads + g * G + hq;
     if (end == beg) {
         *reinterpret_cast<uint2 *>(a.out + row * kD + 4 * d4) = make_uint2(0, 0);
         if (d4 == 0) a.lse[row] = -INFINITY;
         return;
     }
-    const int ca = owner_chunk(beg, T, a.chunks);
-    const int cb = owner_chunk(end - 1, T, a.chunks);
+    const int ca = owner_chunk(beg, W, a.chunks);
+    const int cb = owner_chunk(end - 1, W, a.chunks);
     if (ca == cb) return;  // written by the stream kernel
     auto pidx = [&](int ch, int sl) { return (((int64_t)g * a.chunks + ch) * 2 + sl) * G + hq; };
+    auto empty_chunk = [&](int ch) { return (int64_t)ch * W / a.chunks == (int64_t)(ch + 1) * W / a.chunks; };
     float mx = a.part_lse[pidx(ca, 1)];
     for (int ch = ca + 1; ch <= cb; ++ch)
-        if ((int64_t)ch * T / a.chunks != (int64_t)(ch + 1) * T / a.chunks) mx = fmaxf(mx, a.part_lse[pidx(ch, 0)]);
+        if (!empty_chunk(ch)) mx = fmaxf(mx, a.part_lse[pidx(ch, 0)]);
     const float mu = mx == -INFINITY ? 0.f : mx;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     float wsum = 0.f;
     for (int ch = ca; ch <= cb; ++ch) {
-        // chunks with an empty range (T < P) processed nothing
-        if ((int64_t)ch * T / a.chunks == (int64_t)(ch + 1) * T / a.chunks) continue;
+        if (empty_chunk(ch)) continue;  // a chunk with no windows (W < P) wrote nothing
         const int64_t p = pidx(ch, ch == ca ? 1 : 0);
         const float wgt = exp2_fast((a.part_lse[p] - mu) * kLog2e);
         const float4 o = *reinterpret_cast<const float4 *>(a.part_o + p * kD + 4 * d4);
@@ -550,7 +595,7 @@ extern "C" int ck_suffix_decode(const void *q, const void *k, const void *v, con
     a.v = static_cast<const uint16_t *>(v);
     a.part_o = static_cast<float *>(workspace);
     a.part_lse = a.part_o + parts * kD;
-    a.cu_out = reinterpret_cast<int32_t *>(a.part_lse + parts);
+    a.cw_out = reinterpret_cast<int32_t *>(a.part_lse + parts);
     a.bt_cols = bt_cols;
     a.num_blocks = num_blocks;
     a.num_heads = (int)num_heads;
