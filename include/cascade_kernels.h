@@ -26,6 +26,9 @@
  *   ck_f3_gateup_epilogue <- device entry f3_gateup_epilogue(a, b, workspace, d, m, nHalf,
  *                            k, mode, dStride), OPS/f3_floor/op_kernel/kernel_f3_floor.cpp:319-321,
  *                            launched from OPS/f3_floor/op_host/f3_floor.cpp:123
+ *   ck_cascade_decode     <- the caller-side cascade the reference documents
+ *                            (ascend-kernel/README.md:160-201: fa_fp32_stage1
+ *                            flattened, FIA v2 per suffix, lse_merge) as one call
  */
 #ifndef CASCADE_KERNELS_H
 #define CASCADE_KERNELS_H
@@ -130,6 +133,39 @@ int ck_suffix_decode(const void *q, const void *k, const void *v, const int32_t 
                      int64_t kv_heads, int64_t head_dim, int64_t num_blocks, int64_t block_size,
                      float scale, int64_t kv_cap, int64_t num_splits, void *out, float *lse,
                      void *workspace, int64_t workspace_bytes, void *stream);
+
+/* ============================================================================
+ * Fused cascade decode of B single-token queries that share one prefix.
+ *   q                 bf16 [batch, num_heads, 128]
+ *   prefix_k/v        bf16 [prefix_num_blocks, 128, kv_heads, 128]
+ *   prefix_block_table int32 [1, prefix_bt_cols]; prefix_kv_seqlen int64 [1]
+ *                     on the device (the shared prefix length)
+ *   suffix_k/v        bf16 [suffix_num_blocks, 128, kv_heads, 128] (may be the
+ *                     same pool as the prefix)
+ *   suffix_block_table int32 [batch, suffix_bt_cols]; suffix_kv_seqlens int64
+ *                     [batch] on the device (0 = empty suffix)
+ *   out               bf16 [batch, num_heads, 128]: attention of each query over
+ *                     prefix + its own suffix
+ *   lse_out           fp32 [batch * num_heads]: the merged log-sum-exp
+ *   prefix_cap / suffix_cap  bounds of the kv lengths, <= bt_cols * 128
+ * Arithmetic: stage-1 as ck_fa_fp32_stage1 (bf16 P into the PV product),
+ * suffix as ck_suffix_decode (fp32 P), merge as ck_lse_merge with lse_out;
+ * the stage-1 split partials and cut-suffix partials are folded in fp32
+ * without an intermediate bf16 or fp32 output pass.
+ * Replaces the composition fa_fp32_stage1 -> FIA v2 -> lse_merge of
+ * ascend-kernel/README.md:160-201.
+ * ========================================================================== */
+int ck_cascade_decode_plan(int64_t batch, int64_t num_heads, int64_t kv_heads, int64_t head_dim,
+                           int64_t prefix_cap, int64_t suffix_cap, int64_t *workspace_bytes);
+
+int ck_cascade_decode(const void *q, const void *prefix_k, const void *prefix_v,
+                      const int32_t *prefix_block_table, int64_t prefix_bt_cols,
+                      const int64_t *prefix_kv_seqlen, int64_t prefix_num_blocks, const void *suffix_k,
+                      const void *suffix_v, const int32_t *suffix_block_table, int64_t suffix_bt_cols,
+                      const int64_t *suffix_kv_seqlens, int64_t suffix_num_blocks, int64_t batch,
+                      int64_t num_heads, int64_t kv_heads, int64_t head_dim, int64_t block_size,
+                      float scale, int64_t prefix_cap, int64_t suffix_cap, void *out, float *lse_out,
+                      void *workspace, int64_t workspace_bytes, void *stream);
 
 /* ============================================================================
  * gate_up GEMM with the epilogue ladder of OPS/f3_floor (bf16, fp32 accumulate).

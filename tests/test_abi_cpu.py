@@ -71,3 +71,28 @@ def test_gemm_validation():
     assert L.ck_f3_gateup_epilogue(p, p, p, p, 16, 128, 128, 6, 128, None) == -1  # mode 6
     assert L.ck_f3_gateup_epilogue(p, p, None, p, 16, 128, 128, 0, 128, None) == -2  # mode 0 needs C
     assert L.ck_f3_gateup_epilogue(p, p, p, p, 0, 128, 128, 1, 128, None) == -1   # M = 0
+
+
+def test_cascade_plan_and_validation():
+    w = abi.cascade_plan(64, 32, 8, 128, 8192, 4096)        # the benchmark's cascade shape
+    s1, w1 = abi.stage1_plan(1, 64, 32, 8, 128, 8192)
+    assert w >= w1 + 64 * 32 * (128 * 2 + 4)                 # stage-1 partials + suffix scratch
+    assert abi.cascade_plan(0, 32, 8, 128, 8192, 4096) == 0
+    L = abi.lib()
+    out = ctypes.c_int64(0)
+    assert L.ck_cascade_decode_plan(4, 64, 4, 128, 128, 128, ctypes.byref(out)) == -4   # 16 heads per kv head
+    assert L.ck_cascade_decode_plan(4, 32, 8, 64, 128, 128, ctypes.byref(out)) == -4    # D != 128
+    assert L.ck_cascade_decode_plan(4, 30, 8, 128, 128, 128, ctypes.byref(out)) == -1   # H % KVH
+    assert L.ck_cascade_decode_plan(4, 32, 8, 128, 128, 128, None) == -2
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation first
+
+    def call(batch=4, block=128, pcols=1, pcap=128, scols=1, scap=128, ws=None, wsb=0, q=p):
+        return L.ck_cascade_decode(q, p, p, p, pcols, p, 1, p, p, p, scols, p, 1, batch, 32, 8, 128, block,
+                                   0.088, pcap, scap, p, p, ws, wsb, None)
+    assert call(block=64) == -4                     # block size
+    assert call(pcap=256) == -1                     # prefix bound beyond its table
+    assert call(scap=256) == -1                     # suffix bound beyond its table
+    assert call(q=None) == -2
+    need = abi.cascade_plan(4, 32, 8, 128, 128, 128)
+    assert call(ws=p, wsb=need - 1) == -3           # short workspace, nothing launched
+    assert call(batch=0) == 0                       # empty batch: nothing to do

@@ -120,35 +120,134 @@ def _cascade_inputs(B, H, KVH, P, suf, seed):
     return bf16_bits(q), bf16_bits(k), bf16_bits(v), bt_pre, bt_suf, np.asarray(suf, dtype=np.int64)
 
 
-@pytest.mark.parametrize("cfg", [(8, 8, 2, 1024, "u64_256"), (16, 32, 8, 2048, "geo512"), (4, 32, 8, 512, "with_empty")],
-                         ids=["config1_b8_h8", "b16_h32_geo", "empty_suffix"])
-def test_cascade_equals_dense_over_concat(cfg):
-    """Config 1 shape (and two more): cascade_decode == softmax attention over the
-    concatenated prefix + suffix KV (bf16 output)."""
-    import cascade_amd
+CASCADE_CFGS = [
+    (8, 8, 2, 1024, "u64_256"),      # BASELINE config 1 shape
+    (16, 32, 8, 2048, "geo512"),
+    (4, 32, 8, 512, "with_empty"),
+    (6, 64, 8, 640, "long_cut"),     # G = 8; suffixes cut across workgroups
+    (40, 16, 2, 0, "no_prefix"),     # empty prefix: the suffix alone
+    (3, 8, 8, 256, "all_empty"),     # every suffix empty: the prefix alone
+]
+CASCADE_IDS = ["config1_b8_h8", "b16_h32_geo", "empty_suffix", "gqa8_long_cut", "empty_prefix", "all_suffix_empty"]
+
+
+def _cascade_case(cfg):
     B, H, KVH, P, dist = cfg
     rng = np.random.default_rng(B)
     if dist == "u64_256":
         suf = rng.integers(64, 257, size=B)
     elif dist == "geo512":
         suf = np.clip(rng.geometric(1 / 512, size=B), 1, 4096)
-    else:
+    elif dist == "with_empty":
         suf = np.array([0, 5, 0, 300])
-    q16, k16, v16, bt_pre, bt_suf, suf = _cascade_inputs(B, H, KVH, P, suf, seed=B)
+    elif dist == "long_cut":
+        suf = np.array([4000, 1, 2500, 129, 3333, 64])
+    elif dist == "no_prefix":
+        suf = rng.integers(0, 300, size=B)
+    else:
+        suf = np.zeros(B, dtype=np.int64)
+    return (B, H, KVH, P) + _cascade_inputs(B, H, KVH, P, suf, seed=B)
+
+
+def _cascade_run(fused, B, P, q, k, v, bt_pre, bt_suf, suf):
+    import cascade_amd
+    bt_pre_t = torch.from_numpy(bt_pre if bt_pre.shape[1] else np.zeros((1, 1), np.int32)).to(DEV)
+    plen = torch.tensor([P], dtype=torch.int64, device=DEV)
+    args = (q, k, v, bt_pre_t, plen, k, v, torch.from_numpy(bt_suf).to(DEV), torch.from_numpy(suf).to(DEV))
+    if fused:
+        out, lse = cascade_amd.ops.cascade_decode(*args)
+    else:
+        out, lse = cascade_amd.ops.cascade_decode_unfused(*args), None
+    torch.cuda.synchronize()
+    return bf16_to_np(out), (None if lse is None else lse.cpu().numpy())
+
+
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
+@pytest.mark.parametrize("cfg", CASCADE_CFGS, ids=CASCADE_IDS)
+def test_cascade_equals_dense_over_concat(cfg, fused):
+    """Config 1 shape (and more): cascade decode == softmax attention over the
+    concatenated prefix + suffix KV (bf16 output), for the fused op and for the
+    reference's three-op composition; the fused op's merged LSE matches too."""
+    B, H, KVH, P, q16, k16, v16, bt_pre, bt_suf, suf = _cascade_case(cfg)
+    if not fused and P == 0:
+        pytest.skip("fa_fp32_stage1 requires kv seqlens >= 1 (reference op_host contract)")
     q, k, v = (torch_bf16(x, DEV) for x in (q16, k16, v16))
-    out = cascade_amd.ops.cascade_decode(q, k, v, torch.from_numpy(bt_pre).to(DEV), P, k, v,
-                                         torch.from_numpy(bt_suf).to(DEV), torch.from_numpy(suf).to(DEV))
-    got = bf16_to_np(out)
+    got, lse = _cascade_run(fused, B, P, q, k, v, bt_pre, bt_suf, suf)
     qf, kf, vf = bits_to_f32(q16), bits_to_f32(k16), bits_to_f32(v16)
     for b in range(B):
-        kp, vp = A.gather_kv(kf, vf, bt_pre[0], P)
+        kp, vp = A.gather_kv(kf, vf, bt_pre[0], P) if P else (kf[:0, 0], vf[:0, 0])
         ks, vs = A.gather_kv(kf, vf, bt_suf[b], int(suf[b]))
-        Od, _ = A.dense(qf[b:b + 1], A.expand_heads(np.concatenate([kp, ks]), H),
-                        A.expand_heads(np.concatenate([vp, vs]), H))
+        kc, vc = np.concatenate([kp, ks]), np.concatenate([vp, vs])
+        if kc.shape[0] == 0:
+            assert np.all(got[b] == 0)
+            if lse is not None:
+                assert np.all(np.isneginf(lse.reshape(B, H)[b]))
+            continue
+        Od, Ld = A.dense(qf[b:b + 1], A.expand_heads(kc, H), A.expand_heads(vc, H))
         err = np.abs(got[b:b + 1] - Od)
         assert np.all(err <= 2e-3 + 2.0 ** -8 * np.abs(Od)), (b, err.max())
+        if lse is not None:
+            rel = np.abs(lse.reshape(B, H)[b] - Ld[0]) / np.maximum(np.abs(Ld[0]), 1.0)
+            assert rel.max() <= 1e-4, (b, rel.max())
     # and equals the oracle's own cascade composition
-    O1, L1 = A.stage1(qf, kf, vf, bt_pre, [B], [P])
-    O2, L2 = A.stage1(qf, kf, vf, bt_suf, np.ones(B, dtype=np.int64), suf, quantize_p=False)
-    Om, _ = merge_fp64(O1, O2, L1, L2)
-    assert np.all(np.abs(got - Om) <= 2e-3 + 2.0 ** -8 * np.abs(Om))
+    if P:
+        O1, L1 = A.stage1(qf, kf, vf, bt_pre, [B], [P])
+        O2, L2 = A.stage1(qf, kf, vf, bt_suf, np.ones(B, dtype=np.int64), suf, quantize_p=False)
+        Om, _ = merge_fp64(O1, O2, L1, L2)
+        assert np.all(np.abs(got - Om) <= 2e-3 + 2.0 ** -8 * np.abs(Om))
+
+
+def test_cascade_fused_matches_unfused():
+    """The fused op and the three-op composition differ only by rounding: the
+    composition rounds a cut suffix's result to bf16 before the merge."""
+    B, H, KVH, P, q16, k16, v16, bt_pre, bt_suf, suf = _cascade_case((16, 32, 8, 2048, "geo512"))
+    q, k, v = (torch_bf16(x, DEV) for x in (q16, k16, v16))
+    a, _ = _cascade_run(True, B, P, q, k, v, bt_pre, bt_suf, suf)
+    b, _ = _cascade_run(False, B, P, q, k, v, bt_pre, bt_suf, suf)
+    assert np.all(np.abs(a - b) <= 2.0 ** -7 * np.abs(b) + 1e-3)
+
+
+def test_cascade_two_launch_groups():
+    """More sequences than one suffix launch holds (2048): the fused op runs the
+    suffix and epilogue per group; every row still matches the composition."""
+    B, H, KVH, P = 2100, 8, 2, 256
+    rng = np.random.default_rng(7)
+    suf = rng.integers(0, 80, size=B)
+    q16, k16, v16, bt_pre, bt_suf, suf = _cascade_inputs(B, H, KVH, P, suf, seed=7)
+    q, k, v = (torch_bf16(x, DEV) for x in (q16, k16, v16))
+    a, lse = _cascade_run(True, B, P, q, k, v, bt_pre, bt_suf, suf)
+    b, _ = _cascade_run(False, B, P, q, k, v, bt_pre, bt_suf, suf)
+    assert np.all(np.abs(a - b) <= 2.0 ** -7 * np.abs(b) + 1e-3)
+    assert np.all(np.isfinite(lse))
+
+
+def test_cascade_abi_matches_torch_op():
+    """ck_cascade_decode through ctypes == torch.ops.npu.cascade_decode (bitwise)."""
+    import cascade_amd
+    from cascade_amd import abi
+    B, H, KVH, P, q16, k16, v16, bt_pre, bt_suf, suf = _cascade_case((16, 32, 8, 2048, "geo512"))
+    q, k, v = (torch_bf16(x, DEV) for x in (q16, k16, v16))
+    btp = torch.from_numpy(bt_pre).to(DEV)
+    bts = torch.from_numpy(bt_suf).to(DEV)
+    plen = torch.tensor([P], dtype=torch.int64, device=DEV)
+    sl = torch.from_numpy(suf).to(DEV)
+    pcap, scap = btp.shape[1] * 128, bts.shape[1] * 128
+    wsb = abi.cascade_plan(B, H, KVH, 128, pcap, scap)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    out = torch.empty(B, H, 128, dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty(B * H, dtype=torch.float32, device=DEV)
+    rc = abi.lib().ck_cascade_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), btp.data_ptr(), btp.shape[1],
+                                     plen.data_ptr(), k.shape[0], k.data_ptr(), v.data_ptr(), bts.data_ptr(),
+                                     bts.shape[1], sl.data_ptr(), k.shape[0], B, H, KVH, 128, 128,
+                                     float(np.float32(1 / np.sqrt(128.0))), pcap, scap, out.data_ptr(),
+                                     lse.data_ptr(), ws.data_ptr(), wsb, torch.cuda.current_stream().cuda_stream)
+    abi.check(rc)
+    o2, l2 = cascade_amd.ops.cascade_decode(q, k, v, btp, plen, k, v, bts, sl)
+    torch.cuda.synchronize()
+    assert torch.equal(out, o2) and torch.equal(lse, l2)
+    # a short workspace is refused before anything is launched
+    assert abi.lib().ck_cascade_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), btp.data_ptr(), btp.shape[1],
+                                       plen.data_ptr(), k.shape[0], k.data_ptr(), v.data_ptr(), bts.data_ptr(),
+                                       bts.shape[1], sl.data_ptr(), k.shape[0], B, H, KVH, 128, 128, 0.088,
+                                       pcap, scap, out.data_ptr(), lse.data_ptr(), ws.data_ptr(), wsb - 1,
+                                       torch.cuda.current_stream().cuda_stream) == -3

@@ -108,3 +108,24 @@ def test_gemm_shapes_and_rejections():
         torch.ops.npu.f3_gateup_epilogue(a, b, _bf(4096, 100), None, 1)
     with pytest.raises(RuntimeError, match="d must be bf16"):
         torch.ops.npu.f3_gateup_epilogue(a, b, None, _bf(4096, 100), 1)
+
+
+def test_cascade_shapes_and_rejections():
+    q = _bf(16, 32, 128)
+    kv = _bf(20, 128, 8, 128)
+    btp = torch.empty(1, 4, dtype=torch.int32, device=M)
+    plen = torch.empty(1, dtype=torch.int64, device=M)
+    bts = torch.empty(16, 4, dtype=torch.int32, device=M)
+    sl = torch.empty(16, dtype=torch.int64, device=M)
+    out, lse = torch.ops.npu.cascade_decode(q, kv, kv, btp, plen, kv, kv, bts, sl)
+    assert out.shape == (16, 32, 128) and out.dtype == torch.bfloat16
+    assert lse.shape == (16 * 32,) and lse.dtype == torch.float32
+    with pytest.raises(RuntimeError, match="cascade_decode: the prefix is one request"):
+        torch.ops.npu.cascade_decode(q, kv, kv, btp, torch.empty(2, dtype=torch.int64, device=M), kv, kv, bts, sl)
+    with pytest.raises(RuntimeError, match="cascade_decode: suffix block_table rows"):
+        torch.ops.npu.cascade_decode(q, kv, kv, btp, plen, kv, kv, bts[:3], sl)
+    with pytest.raises(RuntimeError, match="cascade_decode: at most 8 query heads"):
+        kv2 = _bf(20, 128, 2, 128)
+        torch.ops.npu.cascade_decode(_bf(16, 64, 128), kv2, kv2, btp, plen, kv2, kv2, bts, sl)
+    with pytest.raises(RuntimeError, match="cascade_decode: prefix and suffix pools"):
+        torch.ops.npu.cascade_decode(q, kv, kv, btp, plen, _bf(20, 128, 4, 128), _bf(20, 128, 4, 128), bts, sl)

@@ -31,6 +31,9 @@ SIGNATURES = {
     "ck_suffix_decode": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i64,
                                 _i64, _vp, _vp, _vp, _i64, _vp]),
     "ck_f3_gateup_epilogue": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "ck_cascade_decode_plan": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _p64]),
+    "ck_cascade_decode": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
+                                 _i64, _i64, _i64, _f32, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
 }
 
 CK_DTYPE_BF16 = 0
@@ -81,3 +84,10 @@ def suffix_plan(batch, num_heads, kv_heads, head_dim, kv_cap):
     check(lib().ck_suffix_decode_plan(batch, num_heads, kv_heads, head_dim, kv_cap, ctypes.byref(s),
                                       ctypes.byref(w)), "ck_suffix_decode_plan")
     return s.value, w.value
+
+
+def cascade_plan(batch, num_heads, kv_heads, head_dim, prefix_cap, suffix_cap):
+    w = ctypes.c_int64(0)
+    check(lib().ck_cascade_decode_plan(batch, num_heads, kv_heads, head_dim, prefix_cap, suffix_cap,
+                                       ctypes.byref(w)), "ck_cascade_decode_plan")
+    return w.value

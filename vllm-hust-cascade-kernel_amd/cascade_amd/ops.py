@@ -1,9 +1,10 @@
 """Python-facing wrappers over ``torch.ops.npu.*`` (names follow the reference).
 
 ``cascade_decode`` is the caller-side composition the reference documents
-(ascend-kernel/README.md:160-201): stage-1 over the shared prefix in the
-flattened form (one request, q_len = batch, ``q_seqlen_value = batch``), the
-per-sequence suffix attention, and the LSE merge of the two partial results.
+(ascend-kernel/README.md:160-201) -- stage-1 over the shared prefix in the
+flattened form (one request, q_len = batch), the per-sequence suffix attention
+and the LSE merge -- as one fused op; ``cascade_decode_unfused`` composes the
+three separate ops the same way the reference does.
 """
 import torch
 
@@ -34,18 +35,26 @@ def swiglu_gate_up(a, b):
     return torch.ops.npu.f3_gateup_epilogue(a, b, None, None, 1)[0]
 
 
-def cascade_decode(query, prefix_key, prefix_value, prefix_block_table, prefix_len,
-                   suffix_key, suffix_value, suffix_block_table, suffix_kv_seqlens, out_code=1):
-    """Shared-prefix cascade decode for a batch of B single-token queries.
+def cascade_decode(query, prefix_key, prefix_value, prefix_block_table, prefix_kv_seqlens,
+                   suffix_key, suffix_value, suffix_block_table, suffix_kv_seqlens):
+    """Shared-prefix cascade decode for a batch of B single-token queries, fused.
 
     query [B,H,D] bf16; prefix pages shared by all B sequences (prefix_block_table
-    [1, cols]); each sequence's suffix through its own suffix_block_table row.
-    Returns the merged attention output [B,H,D] (bf16 for out_code=1).
+    [1, cols], prefix_kv_seqlens int64 [1] on the device); each sequence's suffix
+    through its own suffix_block_table row and suffix_kv_seqlens entry.
+    Returns (out bf16 [B,H,D], merged LSE fp32 [B*H]).
     """
+    return torch.ops.npu.cascade_decode(query, prefix_key, prefix_value, prefix_block_table, prefix_kv_seqlens,
+                                        suffix_key, suffix_value, suffix_block_table, suffix_kv_seqlens)
+
+
+def cascade_decode_unfused(query, prefix_key, prefix_value, prefix_block_table, prefix_kv_seqlens,
+                           suffix_key, suffix_value, suffix_block_table, suffix_kv_seqlens, out_code=1):
+    """The same cascade as the reference composes it (ascend-kernel/README.md:160-201):
+    stage-1 flattened (one request, q_len = B), suffix attention, lse_merge."""
     B = query.shape[0]
-    dev = query.device
-    qlens = torch.tensor([B], dtype=torch.int64, device=dev)
-    kvlens = torch.tensor([prefix_len], dtype=torch.int64, device=dev)
-    o1, l1 = torch.ops.npu.fa_fp32_stage1(query, prefix_key, prefix_value, prefix_block_table, qlens, kvlens, B)
+    qlens = torch.full((1,), B, dtype=torch.int64, device=query.device)
+    o1, l1 = torch.ops.npu.fa_fp32_stage1(query, prefix_key, prefix_value, prefix_block_table, qlens,
+                                          prefix_kv_seqlens, B)
     o2, l2 = torch.ops.npu.suffix_decode(query, suffix_key, suffix_value, suffix_block_table, suffix_kv_seqlens)
     return torch.ops.npu.lse_merge(o1, o2, l1, l2, out_code)

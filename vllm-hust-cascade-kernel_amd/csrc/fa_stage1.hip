@@ -42,6 +42,7 @@
 // * Block order is XCD-aware: the m-tiles that read the same kv pages are
 //   placed on the same XCD so the second read hits that XCD's L2.
 #include "ck_common.h"
+#include "ck_internal.h"
 
 namespace ck {
 namespace {
@@ -471,14 +472,13 @@ extern "C" int ck_fa_fp32_stage1_plan(int64_t batch, int64_t max_q_len, int64_t 
     return CK_OK;
 }
 
-extern "C" int ck_fa_fp32_stage1(const void *q, const void *k, const void *v, const int32_t *block_table,
-                                 int64_t bt_cols, const int64_t *q_seqlens, const int64_t *kv_seqlens,
-                                 const int32_t *q_start, int64_t batch, int64_t q_len_uniform,
-                                 int64_t max_q_len, int64_t num_tokens, int64_t num_heads,
-                                 int64_t kv_heads, int64_t head_dim, int64_t num_blocks,
-                                 int64_t block_size, float scale, int64_t kv_cap, int64_t num_splits,
-                                 float *out, float *lse, void *workspace, int64_t workspace_bytes,
-                                 void *stream) {
+int ck::stage1_launch(const void *q, const void *k, const void *v, const int32_t *block_table, int64_t bt_cols,
+                      const int64_t *q_seqlens, const int64_t *kv_seqlens, const int32_t *q_start, int64_t batch,
+                      int64_t q_len_uniform, int64_t max_q_len, int64_t num_tokens, int64_t num_heads,
+                      int64_t kv_heads, int64_t head_dim, int64_t num_blocks, int64_t block_size, float scale,
+                      int64_t kv_cap, int64_t num_splits, float *out, float *lse, void *workspace,
+                      int64_t workspace_bytes, bool combine, hipStream_t s, int64_t *splits_used) {
+    if (splits_used) *splits_used = 1;
     int rc = check_dims(batch, max_q_len, num_heads, kv_heads, head_dim, kv_cap);
     if (rc != CK_OK) return rc;
     if (block_size != kPage) return CK_E_UNSUPPORTED;
@@ -493,6 +493,7 @@ extern "C" int ck_fa_fp32_stage1(const void *q, const void *k, const void *v, co
 
     Plan p;
     make_plan(batch, max_q_len, num_heads, kv_heads, kv_cap, num_splits, &p);
+    if (splits_used) *splits_used = p.splits;
     const int64_t need = p.splits > 1 ? p.splits * num_tokens * num_heads * (kD + 1) * (int64_t)sizeof(float) : 0;
     if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return CK_E_WORKSPACE;
 
@@ -524,7 +525,6 @@ extern "C" int ck_fa_fp32_stage1(const void *q, const void *k, const void *v, co
 
     const int64_t grid = batch * kv_heads * p.mtiles * p.splits;
     if (grid <= 0 || grid > 0x7FFFFFFF) return CK_E_INVALID_ARG;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&stage1_kernel),
@@ -535,11 +535,25 @@ extern "C" int ck_fa_fp32_stage1(const void *q, const void *k, const void *v, co
     hipLaunchKernelGGL(stage1_kernel, dim3((unsigned)grid), dim3(kThreads), kLdsBytes, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
-    if (p.splits > 1) {
+    if (p.splits > 1 && combine) {
         const int64_t rows = a.num_rows;
         hipLaunchKernelGGL(stage1_combine_kernel, dim3((unsigned)ceil_div(rows, 8)), dim3(256), 0, s,
                            (const float *)a.part_o, (const float *)a.part_lse, (int)p.splits, rows, out, lse);
         CK_RETURN_LAUNCH();
     }
     return CK_OK;
+}
+
+extern "C" int ck_fa_fp32_stage1(const void *q, const void *k, const void *v, const int32_t *block_table,
+                                 int64_t bt_cols, const int64_t *q_seqlens, const int64_t *kv_seqlens,
+                                 const int32_t *q_start, int64_t batch, int64_t q_len_uniform,
+                                 int64_t max_q_len, int64_t num_tokens, int64_t num_heads,
+                                 int64_t kv_heads, int64_t head_dim, int64_t num_blocks,
+                                 int64_t block_size, float scale, int64_t kv_cap, int64_t num_splits,
+                                 float *out, float *lse, void *workspace, int64_t workspace_bytes,
+                                 void *stream) {
+    return stage1_launch(q, k, v, block_table, bt_cols, q_seqlens, kv_seqlens, q_start, batch, q_len_uniform,
+                         max_q_len, num_tokens, num_heads, kv_heads, head_dim, num_blocks, block_size, scale,
+                         kv_cap, num_splits, out, lse, workspace, workspace_bytes, true,
+                         reinterpret_cast<hipStream_t>(stream), nullptr);
 }

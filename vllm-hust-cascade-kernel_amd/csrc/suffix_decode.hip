@@ -42,6 +42,7 @@
 //   sequence cut by a chunk boundary leaves fp32 partials that a small fix-up
 //   kernel folds (it also writes O = 0, LSE = -inf for empty suffixes).
 #include "ck_common.h"
+#include "ck_internal.h"
 
 namespace ck {
 namespace {
@@ -512,24 +513,150 @@ __global__ __launch_bounds__(256) void suffix_fixup_kernel(SuffixArgs a) {
     if (d4 == 0) a.lse[row] = wsum > 0.f ? mx + __logf(wsum) : -INFINITY;
 }
 
-int64_t ceil_div(int64_t x, int64_t y) { return (x + y - 1) / y; }
+// Cascade epilogue (fused cascade decode): one workgroup per (sequence, kv head),
+// 32 threads x 4 dims per query head. Folds the stage-1 split partials of the
+// sequence's query token, the suffix result (whole, split partials or empty)
+// and merges the two with the lse_merge arithmetic
+//   m = max(l1, l2); w1 = exp(l1 - m); w2 = exp(l2 - m)
+//   out = (o1 w1 + o2 w2) * (1 / (w1 + w2)),  lse = m + log(w1 + w2)
+// (ascend-kernel/csrc/ops/lse_merge/op_kernel/kernel_lse_merge.cpp:237-289);
+// a side at -inf has weight 0, both at -inf give out = 0, lse = -inf.
+struct EpilogueArgs {
+    Stage1Result s1;
+    const uint16_t *o2;     // bf16 [nb][H][kD] whole-sequence suffix results
+    const float *lse2;      // [nb * H]
+    const float *part_o;    // suffix partials [kv_heads][chunks][2][G][kD]
+    const float *part_lse;  // [kv_heads][chunks][2][G]
+    const int32_t *cw;      // [nb + 1] window prefix sums of the group
+    uint16_t *out;          // bf16 [batch][H][kD]
+    float *lse_out;         // [batch * H]
+    int64_t b0;
+    int nb;
+    int num_heads;
+    int kv_heads;
+    int chunks;
+};
 
-// Workgroups per kv head: about one workgroup per CU over the whole grid.
-int64_t suffix_chunks(int64_t kv_heads, int64_t forced) {
-    if (forced > 0) return forced;
-    const int64_t p = 256 / kv_heads;
-    return p > 0 ? p : 1;
+template <int G>
+__global__ __launch_bounds__(256) void cascade_epilogue_kernel(EpilogueArgs e) {
+    constexpr int kBatch = 8;
+    const int bl = blockIdx.x / e.kv_heads;
+    const int g = blockIdx.x % e.kv_heads;
+    const int hq = threadIdx.x >> 5;
+    const int d4 = threadIdx.x & 31;
+    if (hq >= G) return;
+    const int h = g * G + hq;
+    const int64_t row = (e.b0 + bl) * e.num_heads + h;
+
+    // ---- stage 1: the prefix result of this query row ---------------------------
+    float l1;
+    float4 o1;
+    if (e.s1.splits <= 1) {
+        o1 = *reinterpret_cast<const float4 *>(e.s1.o + row * kD + 4 * d4);
+        l1 = e.s1.lse[row * 8];
+    } else {
+        float m = -INFINITY, wsum = 0.f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s0 = 0; s0 < e.s1.splits; s0 += kBatch) {
+            float ls[kBatch];
+            float4 o[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const int s = s0 + j < e.s1.splits ? s0 + j : e.s1.splits - 1;
+                ls[j] = s0 + j < e.s1.splits ? e.s1.lse[(int64_t)s * e.s1.rows + row] : -INFINITY;
+                o[j] = *reinterpret_cast<const float4 *>(e.s1.o + ((int64_t)s * e.s1.rows + row) * kD + 4 * d4);
+            }
+            float mb = m;
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, ls[j]);
+            const float mu = mb == -INFINITY ? 0.f : mb;
+            const float r = exp2_fast((m - mu) * kLog2e);
+            acc.x *= r; acc.y *= r; acc.z *= r; acc.w *= r;
+            wsum *= r;
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const float wgt = exp2_fast((ls[j] - mu) * kLog2e);
+                acc.x = fmaf(wgt, o[j].x, acc.x);
+                acc.y = fmaf(wgt, o[j].y, acc.y);
+                acc.z = fmaf(wgt, o[j].z, acc.z);
+                acc.w = fmaf(wgt, o[j].w, acc.w);
+                wsum += wgt;
+            }
+            m = mb;
+        }
+        const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
+        o1 = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+        l1 = wsum > 0.f ? m + __logf(wsum) : -INFINITY;
+    }
+
+    // ---- suffix: empty, whole (bf16 result) or cut by chunk boundaries ------------
+    float l2 = -INFINITY;
+    float4 o2 = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int64_t beg = e.cw[bl], end = e.cw[bl + 1], W = e.cw[e.nb];
+    if (end > beg) {
+        const int ca = owner_chunk(beg, W, e.chunks);
+        const int cb = owner_chunk(end - 1, W, e.chunks);
+        if (ca == cb) {
+            const int64_t r2 = (int64_t)bl * e.num_heads + h;
+            const uint2 w = *reinterpret_cast<const uint2 *>(e.o2 + r2 * kD + 4 * d4);
+            o2 = make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
+            l2 = e.lse2[r2];
+        } else {
+            auto pidx = [&](int ch, int sl) { return (((int64_t)g * e.chunks + ch) * 2 + sl) * G + hq; };
+            auto empty_chunk = [&](int ch) {
+                return (int64_t)ch * W / e.chunks == (int64_t)(ch + 1) * W / e.chunks;
+            };
+            float mx = e.part_lse[pidx(ca, 1)];
+            for (int ch = ca + 1; ch <= cb; ++ch)
+                if (!empty_chunk(ch)) mx = fmaxf(mx, e.part_lse[pidx(ch, 0)]);
+            const float mu = mx == -INFINITY ? 0.f : mx;
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            float wsum = 0.f;
+            for (int ch = ca; ch <= cb; ++ch) {
+                if (empty_chunk(ch)) continue;
+                const int64_t p = pidx(ch, ch == ca ? 1 : 0);
+                const float wgt = exp2_fast((e.part_lse[p] - mu) * kLog2e);
+                const float4 o = *reinterpret_cast<const float4 *>(e.part_o + p * kD + 4 * d4);
+                acc.x = fmaf(wgt, o.x, acc.x);
+                acc.y = fmaf(wgt, o.y, acc.y);
+                acc.z = fmaf(wgt, o.z, acc.z);
+                acc.w = fmaf(wgt, o.w, acc.w);
+                wsum += wgt;
+            }
+            const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
+            o2 = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+            l2 = wsum > 0.f ? mx + __logf(wsum) : -INFINITY;
+        }
+    }
+
+    // ---- merge --------------------------------------------------------------------
+    const float m = fmaxf(l1, l2);
+    uint2 ow = make_uint2(0, 0);
+    float lse_v = -INFINITY;
+    if (m != -INFINITY) {
+        const float w1 = expf(l1 - m), w2 = expf(l2 - m);
+        const float s = w1 + w2;
+        const float sinv = 1.0f / s;
+        auto mix = [&](float x1, float x2) {
+            const float t1 = (w1 == 0.f) ? 0.f : x1 * w1;
+            const float t2 = (w2 == 0.f) ? 0.f : x2 * w2;
+            return (t1 + t2) * sinv;
+        };
+        ow = make_uint2(pack_bf16x2(mix(o1.x, o2.x), mix(o1.y, o2.y)), pack_bf16x2(mix(o1.z, o2.z), mix(o1.w, o2.w)));
+        lse_v = m + logf(s);
+    }
+    *reinterpret_cast<uint2 *>(e.out + row * kD + 4 * d4) = ow;
+    if (d4 == 0) e.lse_out[row] = lse_v;
 }
 
-int64_t suffix_ws_bytes(int64_t batch, int64_t num_heads, int64_t kv_heads, int64_t chunks) {
-    const int64_t group = num_heads / kv_heads;
-    const int64_t nb = batch < kMaxBatch ? batch : kMaxBatch;
-    const int64_t parts = kv_heads * chunks * 2 * group;
-    return parts * (kD + 1) * (int64_t)sizeof(float) + (nb + 1) * (int64_t)sizeof(int32_t) + 256;
+int64_t ceil_div(int64_t x, int64_t y) { return (x + y - 1) / y; }
+
+int64_t group_parts(int64_t num_heads, int64_t kv_heads, int64_t chunks) {
+    return kv_heads * chunks * 2 * (num_heads / kv_heads);
 }
 
 template <int G>
-int launch_suffix(const SuffixArgs &a, hipStream_t st) {
+int launch_suffix(const SuffixArgs &a, bool fixup, const EpilogueArgs *epi, hipStream_t st) {
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&suffix_stream_kernel<G>),
@@ -542,7 +669,11 @@ int launch_suffix(const SuffixArgs &a, hipStream_t st) {
                        st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
-    hipLaunchKernelGGL(suffix_fixup_kernel<G>, dim3((unsigned)(a.batch * a.kv_heads)), dim3(256), 0, st, a);
+    if (fixup)
+        hipLaunchKernelGGL(suffix_fixup_kernel<G>, dim3((unsigned)(a.batch * a.kv_heads)), dim3(256), 0, st, a);
+    if (epi)
+        hipLaunchKernelGGL(cascade_epilogue_kernel<G>, dim3((unsigned)(a.batch * a.kv_heads)), dim3(256), 0, st,
+                           *epi);
     CK_RETURN_LAUNCH();
 }
 
@@ -557,6 +688,83 @@ int check_suffix_dims(int64_t batch, int64_t num_heads, int64_t kv_heads, int64_
 }
 
 }  // namespace
+
+// Sequences per stream-kernel launch: the window/length prefix sums live in
+// LDS (kMaxBatch entries) and must stay below 2^31 tokens.
+int64_t suffix_group_batch(int64_t kv_cap) {
+    int64_t n = kMaxBatch;
+    const int64_t cap = kv_cap > 0 ? kv_cap : 1;
+    if (n > 0x7FFFFFFF / cap) n = 0x7FFFFFFF / cap;
+    return n < 1 ? 1 : n;
+}
+
+// Workgroups per kv head: about one workgroup per CU over the whole grid.
+int64_t suffix_default_chunks(int64_t kv_heads) {
+    const int64_t p = 256 / kv_heads;
+    return p > 0 ? p : 1;
+}
+
+int64_t suffix_group_ws_bytes(int64_t nb, int64_t num_heads, int64_t kv_heads, int64_t chunks) {
+    const int64_t parts = group_parts(num_heads, kv_heads, chunks);
+    return parts * (kD + 1) * (int64_t)sizeof(float) + (nb + 1) * (int64_t)sizeof(int32_t) + 256;
+}
+
+int suffix_launch_group(const void *q, const void *k, const void *v, const int32_t *block_table, int64_t bt_cols,
+                        const int64_t *kv_seqlens, int64_t b0, int64_t nb, int64_t num_heads, int64_t kv_heads,
+                        int64_t num_blocks, float scale, int64_t kv_cap, int64_t chunks, void *out, float *lse,
+                        void *group_ws, const Stage1Result *cascade, void *final_out, float *final_lse,
+                        hipStream_t stream) {
+    const int64_t group = num_heads / kv_heads;
+    const int64_t parts = group_parts(num_heads, kv_heads, chunks);
+    SuffixArgs a;
+    a.q = static_cast<const uint16_t *>(q) + b0 * num_heads * kD;
+    a.k = static_cast<const uint16_t *>(k);
+    a.v = static_cast<const uint16_t *>(v);
+    a.bt = block_table + b0 * bt_cols;
+    a.kv_seqlens = kv_seqlens + b0;
+    a.out = static_cast<uint16_t *>(out);
+    a.lse = lse;
+    a.part_o = static_cast<float *>(group_ws);
+    a.part_lse = a.part_o + parts * kD;
+    a.cw_out = reinterpret_cast<int32_t *>(a.part_lse + parts);
+    a.bt_cols = bt_cols;
+    a.num_blocks = num_blocks;
+    a.batch = (int)nb;
+    a.num_heads = (int)num_heads;
+    a.kv_heads = (int)kv_heads;
+    a.kv_cap = (int)kv_cap;
+    a.chunks = (int)chunks;
+    a.scale_log2 = scale * kLog2e;
+    EpilogueArgs e;
+    if (cascade) {
+        e.s1 = *cascade;
+        e.o2 = a.out;
+        e.lse2 = a.lse;
+        e.part_o = a.part_o;
+        e.part_lse = a.part_lse;
+        e.cw = a.cw_out;
+        e.out = static_cast<uint16_t *>(final_out);
+        e.lse_out = final_lse;
+        e.b0 = b0;
+        e.nb = (int)nb;
+        e.num_heads = (int)num_heads;
+        e.kv_heads = (int)kv_heads;
+        e.chunks = (int)chunks;
+    }
+    const bool fixup = cascade == nullptr;
+    const EpilogueArgs *ep = cascade ? &e : nullptr;
+    switch (group) {
+        case 1: return launch_suffix<1>(a, fixup, ep, stream);
+        case 2: return launch_suffix<2>(a, fixup, ep, stream);
+        case 3: return launch_suffix<3>(a, fixup, ep, stream);
+        case 4: return launch_suffix<4>(a, fixup, ep, stream);
+        case 5: return launch_suffix<5>(a, fixup, ep, stream);
+        case 6: return launch_suffix<6>(a, fixup, ep, stream);
+        case 7: return launch_suffix<7>(a, fixup, ep, stream);
+        default: return launch_suffix<8>(a, fixup, ep, stream);
+    }
+}
+
 }  // namespace ck
 
 using namespace ck;
@@ -566,9 +774,10 @@ extern "C" int ck_suffix_decode_plan(int64_t batch, int64_t num_heads, int64_t k
     int rc = check_suffix_dims(batch, num_heads, kv_heads, head_dim, kv_cap);
     if (rc != CK_OK) return rc;
     if (!num_splits || !workspace_bytes) return CK_E_NULL_PTR;
-    const int64_t chunks = suffix_chunks(kv_heads, 0);
+    const int64_t chunks = suffix_default_chunks(kv_heads);
+    const int64_t nb = batch < suffix_group_batch(kv_cap) ? batch : suffix_group_batch(kv_cap);
     *num_splits = chunks;
-    *workspace_bytes = batch > 0 ? suffix_ws_bytes(batch, num_heads, kv_heads, chunks) : 0;
+    *workspace_bytes = batch > 0 ? suffix_group_ws_bytes(nb, num_heads, kv_heads, chunks) : 0;
     return CK_OK;
 }
 
@@ -583,51 +792,18 @@ extern "C" int ck_suffix_decode(const void *q, const void *k, const void *v, con
     if (bt_cols < 0 || num_blocks < 0 || kv_cap > bt_cols * kPage) return CK_E_INVALID_ARG;
     if (batch == 0) return CK_OK;
     if (!q || !k || !v || !block_table || !kv_seqlens || !out || !lse) return CK_E_NULL_PTR;
-    const int64_t chunks = suffix_chunks(kv_heads, num_splits);
+    const int64_t chunks = num_splits > 0 ? num_splits : suffix_default_chunks(kv_heads);
     if (kv_heads * chunks > 0x7FFFFFFF || chunks > (1 << 20)) return CK_E_INVALID_ARG;
-    const int64_t need = suffix_ws_bytes(batch, num_heads, kv_heads, chunks);
-    if (workspace == nullptr || workspace_bytes < need) return CK_E_WORKSPACE;
-    const int64_t group = num_heads / kv_heads;
-    const int64_t parts = kv_heads * chunks * 2 * group;
-
-    SuffixArgs a;
-    a.k = static_cast<const uint16_t *>(k);
-    a.v = static_cast<const uint16_t *>(v);
-    a.part_o = static_cast<float *>(workspace);
-    a.part_lse = a.part_o + parts * kD;
-    a.cw_out = reinterpret_cast<int32_t *>(a.part_lse + parts);
-    a.bt_cols = bt_cols;
-    a.num_blocks = num_blocks;
-    a.num_heads = (int)num_heads;
-    a.kv_heads = (int)kv_heads;
-    a.kv_cap = (int)kv_cap;
-    a.chunks = (int)chunks;
-    a.scale_log2 = scale * kLog2e;
+    const int64_t per_launch = suffix_group_batch(kv_cap);
+    const int64_t nbmax = batch < per_launch ? batch : per_launch;
+    if (workspace == nullptr || workspace_bytes < suffix_group_ws_bytes(nbmax, num_heads, kv_heads, chunks))
+        return CK_E_WORKSPACE;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    // sequences are processed in launches of at most kMaxBatch (prefix sums in
-    // LDS), fewer when the token total could overflow the 32-bit sums
-    int64_t per_launch = kMaxBatch;
-    const int64_t cap = kv_cap > 0 ? kv_cap : 1;
-    if (per_launch > 0x7FFFFFFF / cap) per_launch = 0x7FFFFFFF / cap;
-    if (per_launch < 1) per_launch = 1;
     for (int64_t b0 = 0; b0 < batch; b0 += per_launch) {
         const int64_t nb = batch - b0 < per_launch ? batch - b0 : per_launch;
-        a.q = static_cast<const uint16_t *>(q) + b0 * num_heads * kD;
-        a.bt = block_table + b0 * bt_cols;
-        a.kv_seqlens = kv_seqlens + b0;
-        a.out = static_cast<uint16_t *>(out) + b0 * num_heads * kD;
-        a.lse = lse + b0 * num_heads;
-        a.batch = (int)nb;
-        switch (group) {
-            case 1: rc = launch_suffix<1>(a, st); break;
-            case 2: rc = launch_suffix<2>(a, st); break;
-            case 3: rc = launch_suffix<3>(a, st); break;
-            case 4: rc = launch_suffix<4>(a, st); break;
-            case 5: rc = launch_suffix<5>(a, st); break;
-            case 6: rc = launch_suffix<6>(a, st); break;
-            case 7: rc = launch_suffix<7>(a, st); break;
-            default: rc = launch_suffix<8>(a, st); break;
-        }
+        rc = suffix_launch_group(q, k, v, block_table, bt_cols, kv_seqlens, b0, nb, num_heads, kv_heads,
+                                 num_blocks, scale, kv_cap, chunks, static_cast<uint16_t *>(out) + b0 * num_heads * kD,
+                                 lse + b0 * num_heads, workspace, nullptr, nullptr, nullptr, st);
         if (rc != CK_OK) return rc;
     }
     return CK_OK;

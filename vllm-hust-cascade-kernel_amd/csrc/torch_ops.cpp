@@ -279,6 +279,73 @@ std::tuple<at::Tensor, at::Tensor> suffix_decode_impl(const at::Tensor &query, c
 }
 
 // ----------------------------------------------------------------------------
+// cascade_decode (additive): the documented caller-side cascade
+// (ascend-kernel/README.md:160-201) as one op. Shape-only host logic, no
+// device->host traffic: the kv bounds come from the block-table widths.
+// ----------------------------------------------------------------------------
+std::tuple<at::Tensor, at::Tensor> cascade_decode_impl(const at::Tensor &query, const at::Tensor &prefix_key,
+                                                       const at::Tensor &prefix_value,
+                                                       const at::Tensor &prefix_block_table,
+                                                       const at::Tensor &prefix_kv_seqlens,
+                                                       const at::Tensor &suffix_key, const at::Tensor &suffix_value,
+                                                       const at::Tensor &suffix_block_table,
+                                                       const at::Tensor &suffix_kv_seqlens) {
+    for (const at::Tensor *t : {&query, &prefix_key, &prefix_value, &prefix_block_table, &prefix_kv_seqlens,
+                                &suffix_key, &suffix_value, &suffix_block_table, &suffix_kv_seqlens})
+        TORCH_CHECK(t->is_contiguous(), "cascade_decode: all inputs must be contiguous");
+    TORCH_CHECK(query.scalar_type() == at::kBFloat16, "cascade_decode: query must be bf16");
+    TORCH_CHECK(prefix_key.scalar_type() == at::kBFloat16 && prefix_value.scalar_type() == at::kBFloat16 &&
+                    suffix_key.scalar_type() == at::kBFloat16 && suffix_value.scalar_type() == at::kBFloat16,
+                "cascade_decode: key/value must be bf16");
+    TORCH_CHECK(prefix_block_table.scalar_type() == at::kInt && suffix_block_table.scalar_type() == at::kInt,
+                "cascade_decode: block tables must be int32");
+    TORCH_CHECK(prefix_kv_seqlens.scalar_type() == at::kLong && suffix_kv_seqlens.scalar_type() == at::kLong,
+                "cascade_decode: seqlens must be int64");
+    TORCH_CHECK(query.dim() == 3, "cascade_decode: query must be (B, H, D)");
+    TORCH_CHECK(prefix_key.dim() == 4 && prefix_key.sizes() == prefix_value.sizes() && suffix_key.dim() == 4 &&
+                    suffix_key.sizes() == suffix_value.sizes(),
+                "cascade_decode: key/value must be matching (numBlocks, blockSize, KVH, D)");
+    TORCH_CHECK(prefix_block_table.dim() == 2 && prefix_block_table.size(0) >= 1 && prefix_kv_seqlens.numel() == 1,
+                "cascade_decode: the prefix is one request: block_table (1, cols), kv seqlens (1,)");
+    const int64_t batch = query.size(0), num_heads = query.size(1), embed = query.size(2);
+    const int64_t kv_heads = prefix_key.size(2);
+    TORCH_CHECK(suffix_key.size(2) == kv_heads, "cascade_decode: prefix and suffix pools must have the same kv heads");
+    TORCH_CHECK(suffix_block_table.dim() == 2 && suffix_block_table.size(0) == batch &&
+                    suffix_kv_seqlens.numel() == batch,
+                "cascade_decode: suffix block_table rows and kv seqlens must have batch entries");
+    TORCH_CHECK(embed == 128 && prefix_key.size(3) == 128 && suffix_key.size(3) == 128,
+                "cascade_decode: only head dim 128 is supported");
+    TORCH_CHECK(prefix_key.size(1) == 128 && suffix_key.size(1) == 128,
+                "cascade_decode: only paged blockSize 128 is supported");
+    TORCH_CHECK(kv_heads > 0 && num_heads % kv_heads == 0, "cascade_decode: numHeads must be a multiple of kvHeads");
+    TORCH_CHECK(num_heads / kv_heads <= 8, "cascade_decode: at most 8 query heads per kv head are supported");
+    for (const at::Tensor *t : {&prefix_key, &prefix_value, &prefix_block_table, &prefix_kv_seqlens, &suffix_key,
+                                &suffix_value, &suffix_block_table, &suffix_kv_seqlens})
+        TORCH_CHECK(t->device() == query.device(), "cascade_decode: all tensors must be on the same HIP device");
+    TORCH_CHECK(on_device(query), "cascade_decode: tensors must be on a HIP device");
+    auto out = at::empty({batch, num_heads, embed}, query.options());
+    auto lse = at::empty({batch * num_heads}, query.options().dtype(at::kFloat));
+    if (batch == 0 || query.device().is_meta()) return {out, lse};
+    const int64_t pcols = prefix_block_table.size(1), scols = suffix_block_table.size(1);
+    const int64_t prefix_cap = pcols * 128, suffix_cap = scols * 128;
+    c10::OptionalDeviceGuard guard(query.device());
+    int64_t ws_bytes = 0;
+    check_launch(ck_cascade_decode_plan(batch, num_heads, kv_heads, embed, prefix_cap, suffix_cap, &ws_bytes),
+                 "cascade_decode");
+    at::Tensor ws = at::empty({ws_bytes > 0 ? ws_bytes : 1}, query.options().dtype(at::kByte));
+    const float scale = static_cast<float>(1.0 / std::sqrt(1.0 * embed));
+    check_launch(ck_cascade_decode(query.data_ptr(), prefix_key.data_ptr(), prefix_value.data_ptr(),
+                                   prefix_block_table.data_ptr<int32_t>(), pcols,
+                                   prefix_kv_seqlens.data_ptr<int64_t>(), prefix_key.size(0), suffix_key.data_ptr(),
+                                   suffix_value.data_ptr(), suffix_block_table.data_ptr<int32_t>(), scols,
+                                   suffix_kv_seqlens.data_ptr<int64_t>(), suffix_key.size(0), batch, num_heads,
+                                   kv_heads, embed, 128, scale, prefix_cap, suffix_cap, out.data_ptr(),
+                                   lse.data_ptr<float>(), ws.data_ptr(), ws.numel(), stream_of(query)),
+                 "cascade_decode");
+    return {out, lse};
+}
+
+// ----------------------------------------------------------------------------
 // f3_gateup_epilogue: ascend-kernel/csrc/ops/f3_floor/op_host/f3_floor.cpp:59-124
 // ----------------------------------------------------------------------------
 std::tuple<at::Tensor, at::Tensor> f3_gateup_epilogue_impl(const at::Tensor &a, const at::Tensor &b,
@@ -347,6 +414,9 @@ TORCH_LIBRARY_FRAGMENT(npu, m) {
     m.def("lse_merge_with_lse(Tensor o1, Tensor o2, Tensor lse1, Tensor lse2, int out_code=0) -> (Tensor, Tensor)");
     m.def("suffix_decode(Tensor query, Tensor key, Tensor value, Tensor block_table, "
           "Tensor actual_kv_seqlens) -> (Tensor, Tensor)");
+    m.def("cascade_decode(Tensor query, Tensor prefix_key, Tensor prefix_value, Tensor prefix_block_table, "
+          "Tensor prefix_kv_seqlens, Tensor suffix_key, Tensor suffix_value, Tensor suffix_block_table, "
+          "Tensor suffix_kv_seqlens) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(npu, CUDA, m) {
@@ -354,6 +424,7 @@ TORCH_LIBRARY_IMPL(npu, CUDA, m) {
     m.impl("lse_merge_with_lse", TORCH_FN(cascade_amd::lse_merge_with_lse_impl));
     m.impl("fa_fp32_stage1", TORCH_FN(cascade_amd::fa_fp32_stage1_impl));
     m.impl("suffix_decode", TORCH_FN(cascade_amd::suffix_decode_impl));
+    m.impl("cascade_decode", TORCH_FN(cascade_amd::cascade_decode_impl));
     m.impl("f3_gateup_epilogue", TORCH_FN(cascade_amd::f3_gateup_epilogue_impl));
 }
 
@@ -362,5 +433,6 @@ TORCH_LIBRARY_IMPL(npu, Meta, m) {
     m.impl("lse_merge_with_lse", TORCH_FN(cascade_amd::lse_merge_with_lse_impl));
     m.impl("fa_fp32_stage1", TORCH_FN(cascade_amd::fa_fp32_stage1_impl));
     m.impl("suffix_decode", TORCH_FN(cascade_amd::suffix_decode_impl));
+    m.impl("cascade_decode", TORCH_FN(cascade_amd::cascade_decode_impl));
     m.impl("f3_gateup_epilogue", TORCH_FN(cascade_amd::f3_gateup_epilogue_impl));
 }
