@@ -221,10 +221,14 @@ def main():
     }
     dom = max(per_kernel, key=lambda n: per_kernel[n][0])
     dom_gbs = per_kernel[dom][1] / (per_kernel[dom][0] * 1e-3) / 1e9
-    traffic = None
+    # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    # (calibrated against a plain copy of known size)
+    traffic = gemm_traffic = None
     tpath = os.path.join(REPO, "profiles", "pmc_traffic.json")
     if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get(dom)
+        tj = json.load(open(tpath))
+        traffic = tj.get(dom)
+        gemm_traffic = tj.get("f3_gateup_epilogue")
 
     line = {
         "metric": "cascade-decode attn HBM GB/s (% of peak) + SwiGLU GEMM TFLOP/s at 1 MI355X",
@@ -257,7 +261,7 @@ def main():
                      "unit": "GB/s", "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
         "roofline_gemm": {"kernel": "f3_gateup_epilogue mode 1", "bound": "mfma", "achieved": round(gemm_tflops, 1),
                           "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                          "frac": round(gemm_tflops / BF16_PEAK_TFLOPS, 4), "traffic": None},
+                          "frac": round(gemm_tflops / BF16_PEAK_TFLOPS, 4), "traffic": gemm_traffic},
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(torch)
