@@ -15,17 +15,24 @@
 // * D^T = W X^T on v_mfma_f32_32x32x16_bf16: A operand = weight rows, B operand
 //   = activation rows, both K-contiguous in memory, so fragments are 16-byte
 //   LDS reads and each accumulator lane ends up holding 4 consecutive output
-//   columns (8-byte bf16 stores in the epilogue).
-// * Workgroup tile: 256 activation rows x (128 gate + the matching 128 up
-//   weight rows), K step 64, 8 waves arranged 2 (activation) x 4 (weight).
-//   Each wave owns 128 activation rows x (32 gate + 32 up) weight rows, so the
-//   gate and up accumulators of one output element sit in the same lane and
-//   register index: SwiGLU is computed in registers in fp32 and stored once as
-//   bf16 -- the gate/up product never reaches memory.
-// * Operand tiles go global -> registers -> LDS (double buffered, 2 x 64 KB,
-//   16-byte XOR swizzle per 128-byte row so the 32-row MFMA fragment reads are
-//   bank-conflict free); the next K tile's global loads are in flight while the
-//   current tile's 32 MFMAs per wave run.
+//   columns (8-byte bf16 stores in the epilogue). The gate and up accumulators
+//   of one output element sit in the same lane and register index: SwiGLU is
+//   computed in registers in fp32 and stored once as bf16 -- the gate/up
+//   product never reaches memory.
+// * Main kernel (K a multiple of 32): workgroup tile 256 activation rows x
+//   (128 gate + the matching 128 up weight rows), K step 32, 4 waves (one per
+//   SIMD) arranged 2 (activation) x 2 (weight); each wave owns 128 activation
+//   rows x (64 gate + 64 up) weight rows, 16 accumulator tiles of 32x32 in the
+//   accumulation registers, so per 16-deep k-substep 8 fragment reads feed 16
+//   MFMAs (half an LDS read per MFMA). Operand tiles stream global -> LDS by
+//   DMA (global_load_lds_dwordx4: no staging registers, no LDS write
+//   instructions) into a 4 x 32 KB ring, three tiles ahead; each 64-byte row
+//   is XOR-swizzled at 16-byte granularity (the DMA lane fetches the chunk that
+//   belongs at its LDS slot) so the 32-row fragment reads are bank-conflict
+//   free. The fragments of substep s + 1 are read while the
+//   MFMAs of substep s run, interleaved by scheduling barriers.
+// * General kernel (any K % 16 == 0): 8 waves of 128 x (32 + 32), operands
+//   staged global -> registers -> LDS.
 // * Tiles are ordered M-fastest and XCD-aware so the workgroups sharing a
 //   weight slice run on the same XCD and hit its L2.
 #include "ck_common.h"
@@ -63,7 +70,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 }
 
 template <int MODE>
-__global__ __launch_bounds__(kThreads) void gateup_kernel(GemmArgs p) {
+__global__ __launch_bounds__(kThreads) void gateup_general_kernel(GemmArgs p) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int tid = threadIdx.x;
     const int wid = tid >> 6;
@@ -187,6 +194,193 @@ __global__ __launch_bounds__(kThreads) void gateup_kernel(GemmArgs p) {
     }
 }
 
+// ---- main kernel: 4 waves x (128 x 128), DMA-fed 4-stage LDS ring ------------------------
+constexpr int kDThreads = 256;
+constexpr int kDBK = 32;                                  // K per ring stage
+constexpr int kDStages = 4;
+constexpr int kGroupM = 4;   // tile block one XCD runs at once: 4 m-tiles x 8 n-tiles
+constexpr int kGroupN = 8;
+constexpr int kDRowBytes = kDBK * 2;                      // 64 B per staged row
+constexpr int kDStageBytes = (kBM + kBW) * kDRowBytes;    // 32 KB
+constexpr int kDDmaPerWave = kDStageBytes / 1024 / 4;     // 1 KB DMAs per wave per stage (8)
+constexpr int kDLdsBytes = kDStages * kDStageBytes;       // 128 KB
+
+// Byte offset of 16-byte chunk ch of staged row `row`: 64-byte rows, chunk
+// slot ch ^ f(row) with f(row) = ((row >> 1) ^ (row >> 2)) & 3. A fragment read
+// has 32 lanes on consecutive rows at one chunk; with this f the rows that
+// share a bank window -- 4 per 256-byte window (16 lanes per LDS cycle) or 2
+// per 128-byte window -- land on different 16-byte slots, so the read is
+// conflict-free (a plain ((row >> 1) & 3) collides rows r and r + 8).
+__device__ __forceinline__ int dsw_swz(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
+__device__ __forceinline__ int dsw_off(int row, int ch) { return row * kDRowBytes + ((ch ^ dsw_swz(row)) << 4); }
+
+template <int MODE>
+__global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
+    extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+    CK_LDS char *smem = (CK_LDS char *)smem_raw;
+    const int tid = threadIdx.x;
+    const int wid = tid >> 6;
+    const int lane = tid & 63;
+    const int hh = lane >> 5;
+    const int l32 = lane & 31;
+    const int wa = wid >> 1;  // activation half: rows wa*128 .. +128
+    const int ww = wid & 1;   // weight half: gate rows ww*64 .. +64 (and up)
+
+    const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
+    // the 32 workgroups an XCD runs at once (consecutive w after the remap) form
+    // a 4 (m) x 8 (n) block of tiles: 12 operand slices shared through its L2
+    // per K step instead of 18 for a 16 x 2 column
+    int mi, ni;
+    if (p.mtiles % kGroupM == 0 && p.ntiles % kGroupN == 0) {
+        const int grp = w / (kGroupM * kGroupN), in = w % (kGroupM * kGroupN);
+        const int mgroups = p.mtiles / kGroupM;
+        mi = (grp % mgroups) * kGroupM + in % kGroupM;
+        ni = (grp / mgroups) * kGroupN + in / kGroupM;
+    } else {
+        mi = w % p.mtiles;
+        ni = w / p.mtiles;
+    }
+    const int64_t m0 = (int64_t)mi * kBM;
+    const int64_t n0 = (int64_t)ni * kBNh;
+    const int ktiles = (int)(p.k / kDBK);
+
+    // DMA geometry: instruction j of wave w fills staged rows 16*(8w + j) .. +16
+    // (waves 0-1: activations, wave 2: gate rows, wave 3: up rows); lane l ->
+    // row + l/4, LDS slot l%4, which holds global chunk (l%4) ^ f(row); rows of
+    // an instruction start at a multiple of 16, so f(row) = f(l/4).
+    const int rsub = lane >> 2;
+    const int coff = ((lane & 3) ^ dsw_swz(rsub)) * 8;
+    const uint16_t *gp[kDDmaPerWave];
+#pragma unroll
+    for (int j = 0; j < kDDmaPerWave; ++j) {
+        const int R = 16 * (kDDmaPerWave * wid + j) + rsub;
+        int64_t grow;
+        const uint16_t *base;
+        if (R < kBM) {
+            grow = m0 + R;
+            if (grow >= p.m) grow = p.m - 1;  // rows past m only feed output rows that are not stored
+            base = p.a;
+        } else {
+            const int wr = R - kBM;
+            grow = wr < kBNh ? n0 + wr : p.n_half + n0 + (wr - kBNh);
+            base = p.b;
+        }
+        gp[j] = base + grow * p.k + coff;
+    }
+    auto issue = [&](int kt) {
+        CK_LDS char *dst = smem + (kt % kDStages) * kDStageBytes + (kDDmaPerWave * wid) * 1024;
+#pragma unroll
+        for (int j = 0; j < kDDmaPerWave; ++j) dma16(gp[j] + (int64_t)kt * kDBK, dst + j * 1024);
+    };
+    f32x16 acc[4][2][2];
+#pragma unroll
+    for (int ab = 0; ab < 4; ++ab)
+#pragma unroll
+        for (int gb = 0; gb < 2; ++gb)
+#pragma unroll
+            for (int gu = 0; gu < 2; ++gu)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[ab][gb][gu][e] = 0.f;
+
+    auto read_frags = [&](int kt, int s, bf16x8 (&wf)[2][2], bf16x8 (&xf)[4]) {
+        const CK_LDS char *xa = smem + (kt % kDStages) * kDStageBytes;
+        const CK_LDS char *wb = xa + kBM * kDRowBytes;
+        const int ch = 2 * s + hh;
+#pragma unroll
+        for (int gb = 0; gb < 2; ++gb) {
+            wf[gb][0] = *reinterpret_cast<const CK_LDS bf16x8 *>(wb + dsw_off(ww * 64 + gb * 32 + l32, ch));
+            wf[gb][1] = *reinterpret_cast<const CK_LDS bf16x8 *>(wb + dsw_off(kBNh + ww * 64 + gb * 32 + l32, ch));
+        }
+#pragma unroll
+        for (int ab = 0; ab < 4; ++ab)
+            xf[ab] = *reinterpret_cast<const CK_LDS bf16x8 *>(xa + dsw_off(wa * 128 + ab * 32 + l32, ch));
+    };
+
+    // prologue: tiles 0 .. kDStages-2 in flight, tile 0 landed everywhere
+    for (int i = 0; i < kDStages - 1; ++i)
+        if (i < ktiles) issue(i);
+    {
+        const int after = min(kDStages - 2, ktiles - 1);  // tiles issued after tile 0
+        if (after >= 3) wait_vmcnt<3 * kDDmaPerWave>();
+        else if (after == 2) wait_vmcnt<2 * kDDmaPerWave>();
+        else if (after == 1) wait_vmcnt<kDDmaPerWave>();
+        else wait_vmcnt<0>();
+    }
+    __syncthreads();
+    bf16x8 wf[2][2][2], xf[2][4];
+    read_frags(0, 0, wf[0], xf[0]);
+    for (int kt = 0; kt < ktiles; ++kt) {
+        // the slot of tile kt + kDStages - 1 last held tile kt - 1, which every
+        // wave finished before the barrier at the end of the previous iteration
+        if (kt + kDStages - 1 < ktiles) issue(kt + kDStages - 1);
+#pragma unroll
+        for (int s = 0; s < kDBK / 16; ++s) {
+            if (s + 1 < kDBK / 16) read_frags(kt, s + 1, wf[(s + 1) & 1], xf[(s + 1) & 1]);
+#pragma unroll
+            for (int ab = 0; ab < 4; ++ab)
+#pragma unroll
+                for (int gb = 0; gb < 2; ++gb)
+#pragma unroll
+                    for (int gu = 0; gu < 2; ++gu)
+                        acc[ab][gb][gu] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[s & 1][gb][gu], xf[s & 1][ab],
+                                                                                 acc[ab][gb][gu], 0, 0, 0);
+            if (s + 1 < kDBK / 16) {
+                // one fragment read between every two MFMAs
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                }
+            }
+        }
+        // tile kt + 1 must have landed: the DMAs of the tiles issued after it
+        // (at most kDStages - 2) may still be in flight
+        const int after = min(kDStages - 2, ktiles - 2 - kt);
+        if (after >= 3) wait_vmcnt<3 * kDDmaPerWave>();
+        else if (after == 2) wait_vmcnt<2 * kDDmaPerWave>();
+        else if (after == 1) wait_vmcnt<kDDmaPerWave>();
+        else wait_vmcnt<0>();
+        __syncthreads();
+        if (kt + 1 < ktiles) read_frags(kt + 1, 0, wf[0], xf[0]);
+    }
+
+    // ---- epilogue: lane = activation row l32 of block ab; regs 4c..4c+3 of weight
+    // block gb = output columns n0 + ww*64 + gb*32 + 8c + 4hh + 0..3 -------------------
+#pragma unroll
+    for (int ab = 0; ab < 4; ++ab) {
+        const int64_t gm = m0 + wa * 128 + ab * 32 + l32;
+        if (gm >= p.m) continue;
+#pragma unroll
+        for (int gb = 0; gb < 2; ++gb) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int64_t col = n0 + ww * 64 + gb * 32 + 8 * c + 4 * hh;
+                const f32x16 &G = acc[ab][gb][0];
+                const f32x16 &U = acc[ab][gb][1];
+                const float g0 = G[4 * c + 0], g1 = G[4 * c + 1], g2 = G[4 * c + 2], g3 = G[4 * c + 3];
+                const float u0 = U[4 * c + 0], u1 = U[4 * c + 1], u2 = U[4 * c + 2], u3 = U[4 * c + 3];
+                if (MODE == 1) {
+                    const uint2 dv = make_uint2(pack_bf16x2(silu_mul(g0, u0), silu_mul(g1, u1)),
+                                                pack_bf16x2(silu_mul(g2, u2), silu_mul(g3, u3)));
+                    *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = dv;
+                } else {
+                    const uint2 gv = make_uint2(pack_bf16x2(g0, g1), pack_bf16x2(g2, g3));
+                    const uint2 uv = make_uint2(pack_bf16x2(u0, u1), pack_bf16x2(u2, u3));
+                    uint16_t *crow = p.c + gm * (2 * p.n_half);
+                    *reinterpret_cast<uint2 *>(crow + col) = gv;
+                    *reinterpret_cast<uint2 *>(crow + p.n_half + col) = uv;
+                    if (MODE == 0 || MODE == 5)
+                        *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = gv;
+                    else if (MODE == 4)
+                        *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = uv;
+                    else if (MODE == 8)
+                        *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = make_uint2(0, 0);
+                }
+            }
+        }
+    }
+}
+
 // mode 3: d = workspace[:, :I] (epilogue-only rung), 8 columns per thread.
 __global__ __launch_bounds__(256) void gate_window_copy_kernel(const uint16_t *c, uint16_t *d, int64_t m,
                                                                int64_t n_half, int64_t d_stride) {
@@ -205,15 +399,26 @@ __global__ __launch_bounds__(256) void gate_window_copy_kernel(const uint16_t *c
 
 template <int MODE>
 int launch_gemm(const GemmArgs &p, hipStream_t s) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gateup_kernel<MODE>),
+    const int64_t grid = (int64_t)p.mtiles * p.ntiles;
+    if (p.k % kDBK == 0) {
+        static bool attr_set = false;
+        if (!attr_set) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gateup_dma_kernel<MODE>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, kDLdsBytes);
+            if (e != hipSuccess) return static_cast<int>(e);
+            attr_set = true;
+        }
+        hipLaunchKernelGGL((gateup_dma_kernel<MODE>), dim3((unsigned)grid), dim3(kDThreads), kDLdsBytes, s, p);
+        CK_RETURN_LAUNCH();
+    }
+    static bool attr_set_g = false;
+    if (!attr_set_g) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gateup_general_kernel<MODE>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kTileBytes);
         if (e != hipSuccess) return static_cast<int>(e);
-        attr_set = true;
+        attr_set_g = true;
     }
-    const int64_t grid = (int64_t)p.mtiles * p.ntiles;
-    hipLaunchKernelGGL((gateup_kernel<MODE>), dim3((unsigned)grid), dim3(kThreads), 2 * kTileBytes, s, p);
+    hipLaunchKernelGGL((gateup_general_kernel<MODE>), dim3((unsigned)grid), dim3(kThreads), 2 * kTileBytes, s, p);
     CK_RETURN_LAUNCH();
 }
 
