@@ -89,6 +89,8 @@ int ck_lse_merge(const void *o1, int o1_dtype, const void *o2, int o2_dtype,
  *   max_q_len    upper bound of q_len(b) (equals q_len_uniform when that is > 0)
  *   kv_cap       upper bound of kv_seqlens(b), <= bt_cols * 128; tokens beyond
  *                min(kv_seqlens(b), bt_cols * 128) are never read
+ *   scale        softmax scale, finite and > 0 (the reference fixes 1/sqrt(128),
+ *                OPS/fa_fp32_stage1/design.md:73); CK_E_INVALID_ARG otherwise
  *   out          fp32 [num_tokens, num_heads, 128] = softmax(q k^T * scale) v
  *   lse          fp32 [num_tokens * num_heads * 8]; row (t * num_heads + h)
  *                holds 8 identical copies of log(sum exp(q k^T * scale))

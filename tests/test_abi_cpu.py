@@ -51,6 +51,10 @@ def test_stage1_plan_and_validation():
     # a split plan without a workspace
     assert L.ck_fa_fp32_stage1(p, p, p, p, 64, p, p, None, 1, 64, 64, 64, 32, 8, 128, 64, 128, 0.1, 8192, 0,
                                p, p, None, 0, None) == -3
+    # the softmax scale must be finite and > 0 (the row max is taken before scaling)
+    for bad in (0.0, -0.1, float("inf"), float("nan")):
+        assert L.ck_fa_fp32_stage1(p, p, p, p, 1, p, p, None, 1, 1, 1, 1, 8, 8, 128, 1, 128, bad, 128, 1, p, p,
+                                   None, 0, None) == -1, bad
 
 
 def test_suffix_plan_and_validation():

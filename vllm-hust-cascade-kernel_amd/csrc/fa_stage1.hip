@@ -35,12 +35,18 @@
 // * K and V rows are XOR-swizzled at 16-byte granularity (chunk ^ token) by
 //   choosing which global chunk each DMA lane fetches, so MFMA fragment reads
 //   and transpose reads are bank-conflict free.
-// * Softmax runs in the log2 domain (exp2 on the hardware unit, S pre-scaled by
-//   scale*log2(e)); LSE is converted back to natural log.
+// * Softmax runs in the log2 domain (p = exp2(s * scale * log2(e) - m), one
+//   FMA and one exp2 per score); LSE is converted back to natural log.
+// * The epilogue merges the two token halves through LDS and re-lays O out as
+//   whole rows, so each global store writes two contiguous 512-byte rows
+//   (lane-per-row stores of the accumulator layout scatter 32-byte pieces and
+//   run at a fraction of the write bandwidth).
 // * Split-KV fills the chip when batch*kv_heads*m-tiles is small; partial
 //   (O, LSE) pairs are folded by an N-way LSE merge (stage1_combine_kernel).
 // * Block order is XCD-aware: the m-tiles that read the same kv pages are
 //   placed on the same XCD so the second read hits that XCD's L2.
+#include <cmath>
+
 #include "ck_common.h"
 #include "ck_internal.h"
 
@@ -214,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
     float m_run = -INFINITY;
-    float l_run = 0.f;
+    float l_part = 0.f;  // row sum over the tokens of this lane half
 
     for (int i = 0; i < kStages - 1 && i < ntiles; ++i) issue_tile(i);
 
@@ -258,36 +264,35 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
                 const bf16x8 kf = *reinterpret_cast<const CK_LDS bf16x8 *>(kb + tile_off(ktok, 2 * kk + hh));
                 sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sacc, 0, 0, 0);
             }
-            // scale (log2 domain), mask only on a partial tile, row max
+            // row max of the unscaled scores (mask only on a partial tile); the
+            // scale is > 0, so scaling the max gives the max of the scaled scores
             float smax = -INFINITY;
             if (nvalid < kTileN) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int tok = th * 32 + (e & 3) + 8 * (e >> 2) + 4 * hh;
-                    const float sv = tok < nvalid ? sacc[e] * a.scale_log2 : -INFINITY;
-                    sacc[e] = sv;
-                    smax = fmaxf(smax, sv);
+                    if (tok >= nvalid) sacc[e] = -INFINITY;
+                    smax = fmaxf(smax, sacc[e]);
                 }
             } else {
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    sacc[e] *= a.scale_log2;
-                    smax = fmaxf(smax, sacc[e]);
-                }
+                for (int e = 0; e < 16; ++e) smax = fmaxf(smax, sacc[e]);
             }
-            smax = fmaxf(smax, __shfl_xor(smax, 32));
+            smax = fmaxf(smax, __shfl_xor(smax, 32)) * a.scale_log2;
             const float m_new = fmaxf(m_run, smax);
             const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
             const float dm = exp2_fast(m_run - m_use);
+            // p = exp2(s * scale * log2(e) - m): one FMA and one exp2 per score
             float ls = 0.f;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const float p = exp2_fast(sacc[e] - m_use);
+                const float p = exp2_fast(fmaf(sacc[e], a.scale_log2, -m_use));
                 sacc[e] = p;
                 ls += p;
             }
-            ls += __shfl_xor(ls, 32);
-            l_run = l_run * dm + ls;
+            // the two lane halves hold different tokens of the row: their sums
+            // are kept apart and added once after the loop
+            l_part = l_part * dm + ls;
             m_run = m_new;
             // rescale only when some row's max moved (wave-uniform branch)
             if (__builtin_amdgcn_ballot_w64(dm != 1.0f)) {
@@ -315,23 +320,29 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
         }
     }
 
-    // ---- merge the two token halves through LDS (the ring is free now) ----------------
+    // ---- merge the two token halves, then write whole rows --------------------------
+    // The ring is free now. Wave (rb, 1) parks its O^T accumulators in the
+    // 16 KB slab of row block rb; wave (rb, 0) folds them into its own, then
+    // rewrites the slab as 32 normalised fp32 rows of 512 B (16-byte chunks
+    // XOR-swizzled by row) and stores two whole rows per instruction, so every
+    // global store is a full, contiguous 1 KB.
+    const float l_run = l_part + __shfl_xor(l_part, 32);
     __syncthreads();
-    CK_LDS float *xo = (CK_LDS float *)smem;               // [4 rb][16 quads][64 lanes][4]
-    CK_LDS float *xm = xo + 4 * 64 * 64;                   // [4 rb][64 lanes]
+    CK_LDS float *slab = (CK_LDS float *)smem + rb * (32 * kD);  // [16 quads][64 lanes][4]
+    CK_LDS float *xm = (CK_LDS float *)smem + 4 * 32 * kD;  // past the four slabs
     CK_LDS float *xl = xm + 4 * 64;
     if (th == 1) {
 #pragma unroll
         for (int db = 0; db < 4; ++db)
 #pragma unroll
             for (int c4 = 0; c4 < 4; ++c4)
-                *reinterpret_cast<CK_LDS f32x4 *>(xo + ((rb * 16 + db * 4 + c4) * 64 + lane) * 4) =
+                *reinterpret_cast<CK_LDS f32x4 *>(slab + ((db * 4 + c4) * 64 + lane) * 4) =
                     f32x4{oacc[db][4 * c4], oacc[db][4 * c4 + 1], oacc[db][4 * c4 + 2], oacc[db][4 * c4 + 3]};
         xm[rb * 64 + lane] = m_run;
         xl[rb * 64 + lane] = l_run;
     }
     __syncthreads();
-    if (th == 1 || !row_valid) return;
+    if (th == 1 || !wave_active) return;  // wave-uniform
     const float m1 = xm[rb * 64 + lane], l1 = xl[rb * 64 + lane];
     const float mn = fmaxf(m_run, m1);
     const float mu = mn == -INFINITY ? 0.f : mn;
@@ -339,27 +350,41 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
     const float lt = l_run * f0 + l1 * f1;
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     const float lse_v = lt > 0.f ? (mn + __log2f(lt)) * kLn2 : -INFINITY;
-    float *dst;
-    if (a.num_splits == 1) {
-        dst = a.out + qrow * kD;
-        const float4 lv = make_float4(lse_v, lse_v, lse_v, lse_v);
-        *reinterpret_cast<float4 *>(a.lse + qrow * 8 + 4 * hh) = lv;
-    } else {
-        const int64_t prow = (int64_t)sp * a.num_rows + qrow;
-        dst = a.part_o + prow * kD;
-        if (hh == 0) a.part_lse[prow] = lse_v;
-    }
+    f32x4 o1[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) o1[q] = *reinterpret_cast<const CK_LDS f32x4 *>(slab + (q * 64 + lane) * 4);
+    // lane holds row lane%32, dims 32*db + 8*c4 + 4*hh .. +3 = 16-byte chunk 8*db + 2*c4 + hh
+    const int my_row = lane & 31;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int c4 = 0; c4 < 4; ++c4) {
-            const f32x4 o1 = *reinterpret_cast<const CK_LDS f32x4 *>(xo + ((rb * 16 + db * 4 + c4) * 64 + lane) * 4);
-            const float4 o = make_float4((oacc[db][4 * c4 + 0] * f0 + o1[0] * f1) * inv,
-                                         (oacc[db][4 * c4 + 1] * f0 + o1[1] * f1) * inv,
-                                         (oacc[db][4 * c4 + 2] * f0 + o1[2] * f1) * inv,
-                                         (oacc[db][4 * c4 + 3] * f0 + o1[3] * f1) * inv);
-            *reinterpret_cast<float4 *>(dst + db * 32 + 8 * c4 + 4 * hh) = o;
+            const int q = db * 4 + c4;
+            const f32x4 o = f32x4{(oacc[db][4 * c4 + 0] * f0 + o1[q][0] * f1) * inv,
+                                  (oacc[db][4 * c4 + 1] * f0 + o1[q][1] * f1) * inv,
+                                  (oacc[db][4 * c4 + 2] * f0 + o1[q][2] * f1) * inv,
+                                  (oacc[db][4 * c4 + 3] * f0 + o1[q][3] * f1) * inv};
+            const int chunk = (8 * db + 2 * c4 + hh) ^ my_row;
+            *reinterpret_cast<CK_LDS f32x4 *>(slab + my_row * kD + chunk * 4) = o;
         }
+    if (row_valid) {
+        if (a.num_splits == 1) {
+            const float4 lv = make_float4(lse_v, lse_v, lse_v, lse_v);
+            *reinterpret_cast<float4 *>(a.lse + qrow * 8 + 4 * hh) = lv;
+        } else if (hh == 0) {
+            a.part_lse[(int64_t)sp * a.num_rows + qrow] = lse_v;
+        }
+    }
+    // the wave reads back only its own slab: no barrier, the LDS ops of one wave complete in order
+    float *base = a.num_splits == 1 ? a.out : a.part_o + (int64_t)sp * a.num_rows * kD;
+    const int chunk = lane & 31;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int rr = 2 * j + (lane >> 5);  // row within the block
+        const int64_t qr = __shfl((int)qrow, rr);
+        const f32x4 o = *reinterpret_cast<const CK_LDS f32x4 *>(slab + rr * kD + ((chunk ^ rr) * 4));
+        if (wrow0 + rr < rows_b) *reinterpret_cast<f32x4 *>(base + qr * kD + chunk * 4) = o;
+    }
 }
 
 // N-way LSE merge of split partials: 32 threads per row, 4 dims each. One
@@ -486,6 +511,8 @@ int ck::stage1_launch(const void *q, const void *k, const void *v, const int32_t
     if (q_len_uniform > 0 && (max_q_len != q_len_uniform || num_tokens != batch * q_len_uniform))
         return CK_E_INVALID_ARG;
     if (kv_cap > bt_cols * kPage) return CK_E_INVALID_ARG;
+    // the row max is taken on the unscaled scores, which needs scale > 0
+    if (!(scale > 0.f) || !std::isfinite(scale)) return CK_E_INVALID_ARG;
     if (batch == 0 || num_tokens == 0 || max_q_len == 0) return CK_OK;
     if (!q || !k || !v || !block_table || !kv_seqlens || !out || !lse) return CK_E_NULL_PTR;
     if (q_len_uniform == 0 && (!q_seqlens || !q_start)) return CK_E_NULL_PTR;
