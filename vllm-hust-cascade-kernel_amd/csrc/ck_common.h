@@ -106,6 +106,15 @@ __device__ __forceinline__ uint2 lds_read_tr16(const CK_LDS char *p) {
 // 2^x on the hardware exp unit.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max(x[l], x[l ^ 32]) in every lane: v_permlane32_swap exchanges the upper
+// half of its first operand with the lower half of its second, so swapping x
+// with itself leaves x[l ^ 32] in one result and x[l] in the other (a VALU
+// exchange, no LDS round trip).
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // ---- XCD-aware block order ----------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (block b runs on XCD
 // b % 8). Remap so that consecutive logical work ids land on the same XCD and

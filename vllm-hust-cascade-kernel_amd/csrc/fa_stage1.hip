@@ -32,9 +32,14 @@
 //   operand of O^T += V^T P^T; the V^T operand comes from the untransposed V
 //   tile through ds_read_b64_tr_b16, two reads per fragment, whose token order
 //   (0-3, 8-11 | 4-7, 12-15 per 16) is the accumulator's own.
-// * K and V rows are XOR-swizzled at 16-byte granularity (chunk ^ token) by
-//   choosing which global chunk each DMA lane fetches, so MFMA fragment reads
-//   and transpose reads are bank-conflict free.
+// * K and V rows are XOR-swizzled at 16-byte granularity by choosing which
+//   global chunk each DMA lane fetches: chunk c of token t sits at c ^ swz(t),
+//   swz(t) = the 4-bit rotation ((t & 3) << 2) | ((t >> 2) & 3). Over 16
+//   consecutive tokens swz is a bijection (fragment reads: 16 rows, one chunk,
+//   16 distinct bank groups), and over 4 consecutive tokens it differs in bits
+//   2-3 (transpose reads: 4 rows x 4 chunks of one 64-byte group land in 16
+//   distinct bank groups). Both read kinds are bank-conflict free; the plain
+//   t & 15 swizzle leaves the transpose reads 4-way conflicted.
 // * Softmax runs in the log2 domain (p = exp2(s * scale * log2(e) - m), one
 //   FMA and one exp2 per score); LSE is converted back to natural log.
 // * The epilogue merges the two token halves through LDS and re-lays O out as
@@ -103,7 +108,8 @@ __device__ __forceinline__ bf16x8 pack_p(const f32x16 &s, int base) {
 }
 
 // Byte offset of row tok, 16-byte chunk c inside a K or V tile (XOR swizzle).
-__device__ __forceinline__ int tile_off(int tok, int c) { return tok * (kD * 2) + ((c ^ (tok & 15)) << 4); }
+__device__ __forceinline__ int tile_swz(int tok) { return ((tok & 3) << 2) | ((tok >> 2) & 3); }
+__device__ __forceinline__ int tile_off(int tok, int c) { return tok * (kD * 2) + ((c ^ tile_swz(tok)) << 4); }
 
 __device__ __forceinline__ void wait_tiles(int outstanding) {
     // at most `outstanding` later tiles (kDmaPerTile DMAs each) may remain in flight
@@ -144,23 +150,6 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
     const int row0 = mt * kRows;
     if (row0 >= rows_b) return;  // uniform over the workgroup
 
-    int64_t kvl = a.kv_seqlens[b];
-    const int64_t kv_lim = a.bt_cols * kPage;
-    if (kvl > kv_lim) kvl = kv_lim;
-    if (kvl > a.kv_cap) kvl = a.kv_cap;
-    if (kvl < 0 || a.num_blocks <= 0) kvl = 0;  // no pool: nothing to attend to
-    const int kv_lo = sp * a.split_len;  // a multiple of kPage
-    int kv_hi = kv_lo + a.split_len;
-    if (kv_hi > (int)kvl) kv_hi = (int)kvl;
-    const int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + kTileN - 1) / kTileN : 0;
-
-    // page ids of this split -> LDS (one load per page, before any K/V traffic)
-    const int npages = kv_hi > kv_lo ? (kv_hi - kv_lo + kPage - 1) / kPage : 0;
-    for (int pi = tid; pi < npages; pi += kThreads) {
-        const int page = a.bt[(int64_t)b * a.bt_cols + kv_lo / kPage + pi];
-        s_pages[pi] = (page >= 0 && (int64_t)page < a.num_blocks) ? page : -1;
-    }
-
     const int wrow0 = row0 + rb * 32;
     const bool wave_active = wrow0 < rows_b;
     const int r = wrow0 + (lane & 31);
@@ -179,6 +168,28 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
             qf[kk] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
         }
     }
+    // Page ids are read for the split's whole page range inside the table row,
+    // whatever the kv length (only those below it are used), so they, Q and the
+    // kv length are fetched together in one round trip.
+    const int kv_lo = sp * a.split_len;  // a multiple of kPage
+    {
+        const int pg0 = kv_lo / kPage;
+        const int64_t avail = a.bt_cols - pg0;
+        const int pg_n = (int)min((int64_t)(a.split_len / kPage), avail > 0 ? avail : (int64_t)0);
+        for (int pi = tid; pi < pg_n; pi += kThreads) {
+            const int page = a.bt[(int64_t)b * a.bt_cols + pg0 + pi];
+            s_pages[pi] = (page >= 0 && (int64_t)page < a.num_blocks) ? page : -1;
+        }
+    }
+    int64_t kvl = a.kv_seqlens[b];
+    const int64_t kv_lim = a.bt_cols * kPage;
+    if (kvl > kv_lim) kvl = kv_lim;
+    if (kvl > a.kv_cap) kvl = a.kv_cap;
+    if (kvl < 0 || a.num_blocks <= 0) kvl = 0;  // no pool: nothing to attend to
+    int kv_hi = kv_lo + a.split_len;
+    if (kv_hi > (int)kvl) kv_hi = (int)kvl;
+    const int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + kTileN - 1) / kTileN : 0;
+
     // Q and page ids must be resident before the DMA ring starts: the compiler
     // does not count the inline-asm DMAs, so a wait it deferred into the loop
     // would also drain every tile in flight.
@@ -188,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
     const int64_t head_stride = (int64_t)a.kv_heads * kD;
     // DMA lane geometry: one wave instruction moves 4 token rows (1 KB); lane ->
     // token 4*blk + lane/16 and LDS chunk lane%16, which holds global chunk
-    // (lane%16) ^ (token & 15).
+    // (lane%16) ^ tile_swz(token).
     const int dma_tt = lane >> 4;
     const int dma_pc = lane & 15;
 
@@ -206,7 +217,7 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
         for (int j = 0; j < kDmaPerTile / 2; ++j) {
             const int blk = wid * (kDmaPerTile / 2) + j;
             const int tt = blk * 4 + dma_tt;
-            const int c = dma_pc ^ (tt & 15);
+            const int c = dma_pc ^ tile_swz(tt);
             const int64_t off = (tok0 + tt) * head_stride + g * kD + c * 8;
             dma16(a.k + off, kb + blk * 1024);
             dma16(a.v + off, vb + blk * 1024);
@@ -278,7 +289,7 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) smax = fmaxf(smax, sacc[e]);
             }
-            smax = fmaxf(smax, __shfl_xor(smax, 32)) * a.scale_log2;
+            smax = max_xor32(smax) * a.scale_log2;  // the row's other 16 tokens sit in lane l ^ 32
             const float m_new = fmaxf(m_run, smax);
             const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
             const float dm = exp2_fast(m_run - m_use);
