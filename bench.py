@@ -34,6 +34,7 @@ BF16_PEAK_TFLOPS = 2500.0    # MI355X published dense bf16 MFMA peak
 
 B, H, KVH, D, PREFIX, PAGE = 64, 32, 8, 128, 8192, 128
 GEMM_M, GEMM_K, GEMM_I = 4096, 4096, 14336
+NORM_M, NORM_K = 2048, 5120  # add_rms_norm_stats at the reference's prefill-main shape
 ROTATE_BYTES = 2 << 30
 # the kernels each op launches (an op's HIP-event time covers all of them)
 OP_KERNELS = {"fa_fp32_stage1": "stage1_kernel + stage1_combine_kernel",
@@ -198,6 +199,19 @@ def main():
     def gemm(i):
         torch.ops.npu.f3_gateup_epilogue(a, wt, ws, d_out, 1)
 
+    # add_rms_norm_stats inputs, rotated over enough copies to leave the Infinity Cache
+    norm_copies = 8
+    norm_in = [(torch.randn(NORM_M, NORM_K, device=dev) * 0.5).to(torch.bfloat16) for _ in range(2 * norm_copies)]
+    norm_gamma = (1.0 + torch.randn(NORM_K, device=dev) * 0.1).to(torch.bfloat16)
+
+    def norm0(i):
+        j = 2 * (i % norm_copies)
+        return torch.ops.npu.add_rms_norm_stats(norm_in[j], norm_in[j + 1], None, None, 1e-6, 0)
+
+    def norm1(i):
+        j = 2 * (i % norm_copies)
+        return torch.ops.npu.add_rms_norm_stats(norm_in[j], norm_in[j], norm_gamma, None, 1e-6, 1)
+
     def step(i):
         cascade(i)
         gemm(i)
@@ -228,7 +242,8 @@ def main():
     # component timings over the same number of launches each
     n = args.steps
     ms = {"cascade": timed(cascade, n, 0), "cascade_unfused": timed(cascade_unfused, n, 0), "gemm": timed(gemm, n, 0),
-          "stage1": timed(stage1, n, 0), "suffix": timed(suffix, n, 0), "merge": timed(merge, n, 0)}
+          "stage1": timed(stage1, n, 0), "suffix": timed(suffix, n, 0), "merge": timed(merge, n, 0),
+          "norm0": timed(norm0, n, 0), "norm1": timed(norm1, n, 0)}
 
     # HIP-graph batch: one graph holding one fused cascade call per K/V pool copy,
     # replayed back to back (the plugin's graph mode); launch gaps disappear
@@ -301,6 +316,12 @@ def main():
         "cascade_graph_us": round(ms["cascade_graph"] * 1e3, 2),
         "cascade_graph_gbs": round(w["bytes_end_to_end"] / (ms["cascade_graph"] * 1e-3) / 1e9, 2),
         "per_op_us": {n: round(v[0] * 1e3, 2) for n, v in per_kernel.items()},
+        "add_rms_norm_stats": {
+            "shape": [NORM_M, NORM_K], "dtype": "bf16",
+            "mode0_us": round(ms["norm0"] * 1e3, 2),
+            "mode0_gbs": round((3 * NORM_M * NORM_K * 2 + NORM_M * 4) / (ms["norm0"] * 1e-3) / 1e9, 1),
+            "mode1_us": round(ms["norm1"] * 1e3, 2),
+            "mode1_gbs": round((2 * NORM_M * NORM_K * 2 + NORM_K * 2 + NORM_M * 4) / (ms["norm1"] * 1e-3) / 1e9, 1)},
         "swiglu_gemm": {"tflops": round(gemm_tflops, 1), "us": round(ms["gemm"] * 1e3, 1),
                         "pct_of_bf16_peak": round(100.0 * gemm_tflops / BF16_PEAK_TFLOPS, 2)},
         "roofline": {"kernel": dom + " op (" + OP_KERNELS[dom] + ")", "bound": "hbm", "achieved": round(dom_gbs, 2), "peak": HBM_PEAK_GBS,

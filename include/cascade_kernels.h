@@ -29,6 +29,10 @@
  *   ck_cascade_decode     <- the caller-side cascade the reference documents
  *                            (ascend-kernel/README.md:160-201: fa_fp32_stage1
  *                            flattened, FIA v2 per suffix, lse_merge) as one call
+ *   ck_add_rms_norm_stats <- device entries add_rms_norm_stats_{bf16,fp16}(x1, x2, gamma,
+ *                            beta, xOut, rstd, y, mRows, kDim, mode, eps, kInv, hasBeta,
+ *                            batchStats, pairSum), launched from
+ *                            OPS/add_rms_norm_stats/op_host/add_rms_norm_stats.cpp:130-138
  */
 #ifndef CASCADE_KERNELS_H
 #define CASCADE_KERNELS_H
@@ -52,6 +56,7 @@ const char *ck_error_string(int code);
 /* ---- element type tags ------------------------------------------------------ */
 #define CK_DTYPE_BF16 0
 #define CK_DTYPE_F32 1
+#define CK_DTYPE_F16 2
 
 /* ============================================================================
  * LSE merge of two partial attention results, per row r (fp32 arithmetic):
@@ -188,6 +193,30 @@ int ck_cascade_decode(const void *q, const void *prefix_k, const void *prefix_v,
  * ========================================================================== */
 int ck_f3_gateup_epilogue(const void *a, const void *b, void *workspace, void *d, int64_t m,
                           int64_t n_half, int64_t k, int64_t mode, int64_t d_stride, void *stream);
+
+/* ============================================================================
+ * Residual add + RMSNorm statistics (+ apply): the norm stage of the
+ * reference's F2 fusion study (OPS/add_rms_norm_stats/design.md:37-62). Per
+ * row r of the [m_rows, k_dim] inputs, with rd() = rounding to the data dtype:
+ *   mode 0: x_out = rd(x1 + x2);  rstd = 1 / sqrt(mean_k(x_out^2) + eps)
+ *   mode 1: rstd from x1 (the already rounded residual);
+ *           y = rd(rd(x1 * rstd) * gamma + beta)          (beta NULL = no bias)
+ *   mode 2: rstd of rd(x1 + x2) only
+ *   x1, x2, x_out, y  [m_rows, k_dim] contiguous, dtype CK_DTYPE_BF16 or CK_DTYPE_F16
+ *   gamma, beta       [k_dim], same dtype (mode 1)
+ *   rstd              fp32 [ceil(m_rows / 8) * 8]; rows >= m_rows are written 0
+ * x2 is not read in mode 1; x_out is written in mode 0 only, y in mode 1 only.
+ * The statistics and the apply products are evaluated in fp64 and every rd()
+ * goes fp64 -> fp32 -> dtype (RNE twice), as the reference's fp64 model casts
+ * (OPS/add_rms_norm_stats/test/add_rms_norm_stats_ref.py:139-156).
+ * Domain: 0 < k_dim <= 5120, k_dim % 16 == 0, m_rows >= 0, eps > 0 and finite,
+ * mode in {0, 1, 2}.
+ * Replaces the device entries add_rms_norm_stats_{bf16,fp16} of
+ * OPS/add_rms_norm_stats/op_kernel/kernel_add_rms_norm_stats.cpp:453.
+ * ========================================================================== */
+int ck_add_rms_norm_stats(const void *x1, const void *x2, const void *gamma, const void *beta,
+                          void *x_out, float *rstd, void *y, int64_t m_rows, int64_t k_dim,
+                          int dtype, int64_t mode, double eps, void *stream);
 
 #ifdef __cplusplus
 }

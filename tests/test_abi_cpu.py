@@ -100,3 +100,17 @@ def test_cascade_plan_and_validation():
     need = abi.cascade_plan(4, 32, 8, 128, 128, 128)
     assert call(ws=p, wsb=need - 1) == -3           # short workspace, nothing launched
     assert call(batch=0) == 0                       # empty batch: nothing to do
+
+
+def test_add_rms_norm_validation_without_launch():
+    L = abi.lib()
+    p = ctypes.c_void_p(16)
+    bf16, f16, f32 = abi.CK_DTYPE_BF16, abi.CK_DTYPE_F16, abi.CK_DTYPE_F32
+    assert L.ck_add_rms_norm_stats(p, p, p, None, p, p, p, 4, 40, bf16, 0, 1e-6, None) == -1    # K % 16
+    assert L.ck_add_rms_norm_stats(p, p, p, None, p, p, p, 4, 5136, bf16, 0, 1e-6, None) == -1  # K > 5120
+    assert L.ck_add_rms_norm_stats(p, p, p, None, p, p, p, 4, 64, f32, 0, 1e-6, None) == -1     # dtype
+    assert L.ck_add_rms_norm_stats(p, p, p, None, p, p, p, 4, 64, f16, 3, 1e-6, None) == -1     # mode
+    assert L.ck_add_rms_norm_stats(p, p, p, None, p, p, p, 4, 64, bf16, 0, 0.0, None) == -1     # eps
+    assert L.ck_add_rms_norm_stats(p, None, p, None, p, p, p, 4, 64, bf16, 0, 1e-6, None) == -2  # x2 in mode 0
+    assert L.ck_add_rms_norm_stats(p, p, None, None, p, p, p, 4, 64, bf16, 1, 1e-6, None) == -2  # gamma in mode 1
+    assert L.ck_add_rms_norm_stats(None, None, None, None, None, None, None, 0, 64, bf16, 1, 1e-6, None) == 0

@@ -147,3 +147,14 @@ def test_graph_swiglu_gemm():
     # mode 1 writes only d (the fused epilogue never stores C); mode 2 writes C into the workspace
     _replay_check(make, lambda a, b: torch.ops.npu.f3_gateup_epilogue(a, b, None, None, 1)[0])
     _replay_check(make, lambda a, b: torch.ops.npu.f3_gateup_epilogue(a, b, None, None, 2)[1])
+
+
+def test_graph_add_rms_norm_stats():
+    M, K = 96, 1024
+
+    def make(seed):
+        rng = np.random.default_rng(50 + seed)
+        return [_bf16(rng, (M, K), 0.5), _bf16(rng, (M, K), 0.5), _bf16(rng, (K,), 0.1)]
+
+    for mode in (0, 1, 2):
+        _replay_check(make, lambda x1, x2, gm: torch.ops.npu.add_rms_norm_stats(x1, x2, gm, None, 1e-6, mode))

@@ -20,6 +20,7 @@ _int = ctypes.c_int
 _vp = ctypes.c_void_p
 _f32 = ctypes.c_float
 _p64 = ctypes.POINTER(ctypes.c_int64)
+_f64 = ctypes.c_double
 
 SIGNATURES = {
     "ck_error_string": (ctypes.c_char_p, [_int]),
@@ -34,10 +35,12 @@ SIGNATURES = {
     "ck_cascade_decode_plan": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _p64]),
     "ck_cascade_decode": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
                                  _i64, _i64, _i64, _f32, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
+    "ck_add_rms_norm_stats": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _int, _i64, _f64, _vp]),
 }
 
 CK_DTYPE_BF16 = 0
 CK_DTYPE_F32 = 1
+CK_DTYPE_F16 = 2
 
 _lib = None
 

@@ -30,6 +30,11 @@ def f3_gateup_epilogue(a, b, workspace=None, out_d=None, mode=1):
     return torch.ops.npu.f3_gateup_epilogue(a, b, workspace, out_d, mode)
 
 
+def add_rms_norm_stats(x1, x2, gamma=None, beta=None, eps=1e-6, mode=0):
+    """Residual add + RMSNorm statistics (+ apply); see include/cascade_kernels.h."""
+    return torch.ops.npu.add_rms_norm_stats(x1, x2, gamma, beta, eps, mode)
+
+
 def swiglu_gate_up(a, b):
     """D = silu(a @ b[:I].T) * (a @ b[I:].T) in one fused GEMM (mode 1)."""
     return torch.ops.npu.f3_gateup_epilogue(a, b, None, None, 1)[0]

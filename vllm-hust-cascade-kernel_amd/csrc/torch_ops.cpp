@@ -1,7 +1,7 @@
 // torch_ops.cpp - PyTorch-ROCm custom-op layer over the C ABI (cascade_kernels.h).
 //
 // Registers the reference's op schemas verbatim under namespace `npu`
-// (ascend-kernel/csrc/register.cpp:24-31) plus two additive ops, with the
+// (ascend-kernel/csrc/register.cpp:24-31) plus three additive ops, with the
 // implementations on the CUDA dispatch key (HIP devices on PyTorch-ROCm) and a
 // Meta implementation for shape inference. Validation mirrors the reference's
 // op_host TORCH_CHECKs and their "<op>: ..." messages; every launch goes to the
@@ -400,6 +400,58 @@ std::tuple<at::Tensor, at::Tensor> f3_gateup_epilogue_impl(const at::Tensor &a, 
     return {d, ws};
 }
 
+// ----------------------------------------------------------------------------
+// add_rms_norm_stats: ascend-kernel/csrc/ops/add_rms_norm_stats/op_host/add_rms_norm_stats.cpp:65-141
+// ----------------------------------------------------------------------------
+std::tuple<at::Tensor, at::Tensor, at::Tensor> add_rms_norm_stats_impl(const at::Tensor &x1, const at::Tensor &x2,
+                                                                        const c10::optional<at::Tensor> &gamma,
+                                                                        const c10::optional<at::Tensor> &beta,
+                                                                        double eps, int64_t mode) {
+    constexpr int64_t kMaxK = 5120, kRstdGroup = 8;
+    TORCH_CHECK(x1.dim() == 2, "add_rms_norm_stats: x1 must be 2D (M, K)");
+    TORCH_CHECK(x1.is_contiguous(), "add_rms_norm_stats: x1 must be contiguous");
+    TORCH_CHECK(mode >= 0 && mode <= 2, "add_rms_norm_stats: mode must be 0, 1 or 2");
+    TORCH_CHECK(eps > 0.0, "add_rms_norm_stats: eps must be > 0");
+    const bool is_bf16 = x1.scalar_type() == at::kBFloat16;
+    TORCH_CHECK(is_bf16 || x1.scalar_type() == at::kHalf, "add_rms_norm_stats: x1 must be bf16 or fp16");
+    if (mode != 1) {
+        TORCH_CHECK(x2.defined() && x2.is_contiguous() && x2.sizes() == x1.sizes() &&
+                        x2.scalar_type() == x1.scalar_type(),
+                    "add_rms_norm_stats: x2 must be contiguous, same shape and dtype as x1");
+        TORCH_CHECK(x2.device() == x1.device(), "add_rms_norm_stats: x2 must be on the device of x1");
+    }
+    const int64_t m_rows = x1.size(0), k_dim = x1.size(1);
+    TORCH_CHECK(m_rows > 0, "add_rms_norm_stats: empty row count");
+    TORCH_CHECK(k_dim > 0 && k_dim <= kMaxK, "add_rms_norm_stats: K must be in (0, ", kMaxK, "] (one row per wave)");
+    TORCH_CHECK(k_dim % 16 == 0, "add_rms_norm_stats: K must be a multiple of 16 (32B row copies)");
+    const bool has_beta = mode == 1 && beta.has_value() && beta->defined() && beta->numel() > 0;
+    if (mode == 1) {
+        TORCH_CHECK(gamma.has_value() && gamma->defined() && gamma->is_contiguous() && gamma->numel() == k_dim &&
+                        gamma->scalar_type() == x1.scalar_type(),
+                    "add_rms_norm_stats: mode 1 needs a contiguous gamma of K elements, same dtype");
+        TORCH_CHECK(gamma->device() == x1.device(), "add_rms_norm_stats: gamma must be on the device of x1");
+        if (has_beta) {
+            TORCH_CHECK(beta->is_contiguous() && beta->numel() == k_dim && beta->scalar_type() == x1.scalar_type(),
+                        "add_rms_norm_stats: beta must be contiguous, K elements, same dtype");
+            TORCH_CHECK(beta->device() == x1.device(), "add_rms_norm_stats: beta must be on the device of x1");
+        }
+    }
+    TORCH_CHECK(on_device(x1), "add_rms_norm_stats: x1 must be on a HIP device");
+    const int64_t m_pad = (m_rows + kRstdGroup - 1) / kRstdGroup * kRstdGroup;
+    at::Tensor x_out = mode == 0 ? at::empty_like(x1) : at::empty({0}, x1.options());
+    at::Tensor rstd = at::empty({m_pad, 1}, x1.options().dtype(at::kFloat));
+    at::Tensor y = mode == 1 ? at::empty_like(x1) : at::empty({0}, x1.options());
+    if (x1.device().is_meta()) return {x_out, rstd, y};
+    c10::OptionalDeviceGuard guard(x1.device());
+    check_launch(ck_add_rms_norm_stats(x1.data_ptr(), mode != 1 ? x2.data_ptr() : nullptr,
+                                       mode == 1 ? gamma->data_ptr() : nullptr, has_beta ? beta->data_ptr() : nullptr,
+                                       mode == 0 ? x_out.data_ptr() : nullptr, rstd.data_ptr<float>(),
+                                       mode == 1 ? y.data_ptr() : nullptr, m_rows, k_dim,
+                                       is_bf16 ? CK_DTYPE_BF16 : CK_DTYPE_F16, mode, eps, stream_of(x1)),
+                 "add_rms_norm_stats");
+    return {x_out, rstd, y};
+}
+
 }  // namespace
 }  // namespace cascade_amd
 
@@ -410,6 +462,8 @@ TORCH_LIBRARY_FRAGMENT(npu, m) {
           "Tensor actual_q_seqlens, Tensor actual_kv_seqlens, int q_seqlen_value=0) -> (Tensor, Tensor)");
     m.def("f3_gateup_epilogue(Tensor a, Tensor b, Tensor? workspace, Tensor? out_d, int mode) "
           "-> (Tensor, Tensor)");
+    m.def("add_rms_norm_stats(Tensor x1, Tensor x2, Tensor? gamma, Tensor? beta, float eps, "
+          "int mode) -> (Tensor, Tensor, Tensor)");
     // Additive ops (no reference counterpart in the wheel).
     m.def("lse_merge_with_lse(Tensor o1, Tensor o2, Tensor lse1, Tensor lse2, int out_code=0) -> (Tensor, Tensor)");
     m.def("suffix_decode(Tensor query, Tensor key, Tensor value, Tensor block_table, "
@@ -426,6 +480,7 @@ TORCH_LIBRARY_IMPL(npu, CUDA, m) {
     m.impl("suffix_decode", TORCH_FN(cascade_amd::suffix_decode_impl));
     m.impl("cascade_decode", TORCH_FN(cascade_amd::cascade_decode_impl));
     m.impl("f3_gateup_epilogue", TORCH_FN(cascade_amd::f3_gateup_epilogue_impl));
+    m.impl("add_rms_norm_stats", TORCH_FN(cascade_amd::add_rms_norm_stats_impl));
 }
 
 TORCH_LIBRARY_IMPL(npu, Meta, m) {
@@ -435,4 +490,5 @@ TORCH_LIBRARY_IMPL(npu, Meta, m) {
     m.impl("suffix_decode", TORCH_FN(cascade_amd::suffix_decode_impl));
     m.impl("cascade_decode", TORCH_FN(cascade_amd::cascade_decode_impl));
     m.impl("f3_gateup_epilogue", TORCH_FN(cascade_amd::f3_gateup_epilogue_impl));
+    m.impl("add_rms_norm_stats", TORCH_FN(cascade_amd::add_rms_norm_stats_impl));
 }
