@@ -58,6 +58,11 @@ const char *ck_error_string(int code);
 #define CK_DTYPE_F32 1
 #define CK_DTYPE_F16 2
 
+/* ---- paged K/V pool layouts (block size 128, head dim 128) ----------------- */
+#define CK_KV_NHD 0   /* [num_blocks, 128 tokens, kv_heads, 128]: the stage-1 pool  */
+#define CK_KV_BNSD 1  /* [num_blocks, kv_heads, 128 tokens, 128]: the reference's
+                         stage-2 pool (ascend-kernel/README.md:182-183)           */
+
 /* ============================================================================
  * LSE merge of two partial attention results, per row r (fp32 arithmetic):
  *   m = max(l1, l2); w1 = exp(l1 - m); w2 = exp(l2 - m); s = w1 + w2
@@ -122,7 +127,9 @@ int ck_fa_fp32_stage1(const void *q, const void *k, const void *v, const int32_t
  * Per-sequence paged decode attention over each sequence's own suffix
  * (one query token per sequence, GQA, no MFMA).
  *   q            bf16 [batch, num_heads, 128]
- *   k, v         bf16 [num_blocks, 128, kv_heads, 128]
+ *   k, v         bf16 paged pool in layout kv_layout: CK_KV_NHD
+ *                [num_blocks, 128, kv_heads, 128] or CK_KV_BNSD
+ *                [num_blocks, kv_heads, 128, 128] (same results)
  *   block_table  int32 [batch, bt_cols]; kv_seqlens int64 [batch] on the device
  *   out          bf16 [batch, num_heads, 128]
  *   lse          fp32 [batch * num_heads] (compact); a sequence with kv length 0
@@ -138,7 +145,7 @@ int ck_suffix_decode_plan(int64_t batch, int64_t num_heads, int64_t kv_heads, in
 int ck_suffix_decode(const void *q, const void *k, const void *v, const int32_t *block_table,
                      int64_t bt_cols, const int64_t *kv_seqlens, int64_t batch, int64_t num_heads,
                      int64_t kv_heads, int64_t head_dim, int64_t num_blocks, int64_t block_size,
-                     float scale, int64_t kv_cap, int64_t num_splits, void *out, float *lse,
+                     int64_t kv_layout, float scale, int64_t kv_cap, int64_t num_splits, void *out, float *lse,
                      void *workspace, int64_t workspace_bytes, void *stream);
 
 /* ============================================================================
@@ -147,8 +154,9 @@ int ck_suffix_decode(const void *q, const void *k, const void *v, const int32_t 
  *   prefix_k/v        bf16 [prefix_num_blocks, 128, kv_heads, 128]
  *   prefix_block_table int32 [1, prefix_bt_cols]; prefix_kv_seqlen int64 [1]
  *                     on the device (the shared prefix length)
- *   suffix_k/v        bf16 [suffix_num_blocks, 128, kv_heads, 128] (may be the
- *                     same pool as the prefix)
+ *   suffix_k/v        bf16 suffix pool in layout suffix_kv_layout (CK_KV_NHD,
+ *                     or CK_KV_BNSD [suffix_num_blocks, kv_heads, 128, 128]);
+ *                     an NHD suffix pool may be the prefix pool itself
  *   suffix_block_table int32 [batch, suffix_bt_cols]; suffix_kv_seqlens int64
  *                     [batch] on the device (0 = empty suffix)
  *   out               bf16 [batch, num_heads, 128]: attention of each query over
@@ -169,7 +177,8 @@ int ck_cascade_decode(const void *q, const void *prefix_k, const void *prefix_v,
                       const int32_t *prefix_block_table, int64_t prefix_bt_cols,
                       const int64_t *prefix_kv_seqlen, int64_t prefix_num_blocks, const void *suffix_k,
                       const void *suffix_v, const int32_t *suffix_block_table, int64_t suffix_bt_cols,
-                      const int64_t *suffix_kv_seqlens, int64_t suffix_num_blocks, int64_t batch,
+                      const int64_t *suffix_kv_seqlens, int64_t suffix_num_blocks,
+                      int64_t suffix_kv_layout, int64_t batch,
                       int64_t num_heads, int64_t kv_heads, int64_t head_dim, int64_t block_size,
                       float scale, int64_t prefix_cap, int64_t suffix_cap, void *out, float *lse_out,
                       void *workspace, int64_t workspace_bytes, void *stream);

@@ -64,7 +64,8 @@ def test_suffix_plan_and_validation():
     out = ctypes.c_int64(0)
     assert L.ck_suffix_decode_plan(4, 64, 4, 128, 100, ctypes.byref(out), ctypes.byref(out)) == -4  # group 16
     p = ctypes.c_void_p(16)
-    assert L.ck_suffix_decode(p, p, p, p, 1, p, 0, 8, 8, 128, 1, 128, 0.1, 128, 1, p, p, None, 0, None) == 0
+    assert L.ck_suffix_decode(p, p, p, p, 1, p, 0, 8, 8, 128, 1, 128, 0, 0.1, 128, 1, p, p, None, 0, None) == 0
+    assert L.ck_suffix_decode(p, p, p, p, 1, p, 4, 8, 8, 128, 1, 128, 2, 0.1, 128, 1, p, p, p, 1 << 20, None) == -1
 
 
 def test_gemm_validation():
@@ -90,13 +91,14 @@ def test_cascade_plan_and_validation():
     assert L.ck_cascade_decode_plan(4, 32, 8, 128, 128, 128, None) == -2
     p = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation first
 
-    def call(batch=4, block=128, pcols=1, pcap=128, scols=1, scap=128, ws=None, wsb=0, q=p):
-        return L.ck_cascade_decode(q, p, p, p, pcols, p, 1, p, p, p, scols, p, 1, batch, 32, 8, 128, block,
+    def call(batch=4, block=128, pcols=1, pcap=128, scols=1, scap=128, ws=None, wsb=0, q=p, layout=0):
+        return L.ck_cascade_decode(q, p, p, p, pcols, p, 1, p, p, p, scols, p, 1, layout, batch, 32, 8, 128, block,
                                    0.088, pcap, scap, p, p, ws, wsb, None)
     assert call(block=64) == -4                     # block size
     assert call(pcap=256) == -1                     # prefix bound beyond its table
     assert call(scap=256) == -1                     # suffix bound beyond its table
     assert call(q=None) == -2
+    assert call(layout=2) == -1                     # unknown suffix pool layout
     need = abi.cascade_plan(4, 32, 8, 128, 128, 128)
     assert call(ws=p, wsb=need - 1) == -3           # short workspace, nothing launched
     assert call(batch=0) == 0                       # empty batch: nothing to do

@@ -95,7 +95,7 @@ def test_suffix_abi_matches_torch_op():
     out = torch.empty(4, 32, 128, dtype=torch.bfloat16, device=DEV)
     lse = torch.empty(4 * 32, dtype=torch.float32, device=DEV)
     rc = abi.lib().ck_suffix_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), bt.shape[1],
-                                    kvs.data_ptr(), 4, 32, 8, 128, k.shape[0], 128,
+                                    kvs.data_ptr(), 4, 32, 8, 128, k.shape[0], 128, abi.CK_KV_NHD,
                                     float(np.float32(1 / np.sqrt(128))), cap, s, out.data_ptr(), lse.data_ptr(),
                                     ws.data_ptr(), wsb, torch.cuda.current_stream().cuda_stream)
     abi.check(rc)
@@ -238,7 +238,7 @@ def test_cascade_abi_matches_torch_op():
     lse = torch.empty(B * H, dtype=torch.float32, device=DEV)
     rc = abi.lib().ck_cascade_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), btp.data_ptr(), btp.shape[1],
                                      plen.data_ptr(), k.shape[0], k.data_ptr(), v.data_ptr(), bts.data_ptr(),
-                                     bts.shape[1], sl.data_ptr(), k.shape[0], B, H, KVH, 128, 128,
+                                     bts.shape[1], sl.data_ptr(), k.shape[0], abi.CK_KV_NHD, B, H, KVH, 128, 128,
                                      float(np.float32(1 / np.sqrt(128.0))), pcap, scap, out.data_ptr(),
                                      lse.data_ptr(), ws.data_ptr(), wsb, torch.cuda.current_stream().cuda_stream)
     abi.check(rc)
@@ -248,6 +248,44 @@ def test_cascade_abi_matches_torch_op():
     # a short workspace is refused before anything is launched
     assert abi.lib().ck_cascade_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), btp.data_ptr(), btp.shape[1],
                                        plen.data_ptr(), k.shape[0], k.data_ptr(), v.data_ptr(), bts.data_ptr(),
-                                       bts.shape[1], sl.data_ptr(), k.shape[0], B, H, KVH, 128, 128, 0.088,
+                                       bts.shape[1], sl.data_ptr(), k.shape[0], abi.CK_KV_NHD, B, H, KVH, 128, 128, 0.088,
                                        pcap, scap, out.data_ptr(), lse.data_ptr(), ws.data_ptr(), wsb - 1,
                                        torch.cuda.current_stream().cuda_stream) == -3
+
+
+def _bnsd(pool):
+    """NHD [nb, 128, KVH, D] -> BNSD [nb, KVH, 128, D] copy of the same pages."""
+    return pool.permute(0, 2, 1, 3).contiguous()
+
+
+@pytest.mark.parametrize("case", SUFFIX_CASES[:4], ids=[c[0] for c in SUFFIX_CASES[:4]])
+def test_suffix_bnsd_layout_matches_nhd(case):
+    """The BNSD pool layout (the reference's stage-2 input, ascend-kernel/README.md:182-183)
+    reads the same rows through other strides: results are bit-identical to NHD."""
+    name, B, kvs, H, KVH = case
+    inp = paged_inputs(B, kvs, H, KVH, seed=len(name) + 7, permute=True)
+    q = torch_bf16(inp["q16"], DEV)
+    k = torch_bf16(inp["k16"], DEV)
+    v = torch_bf16(inp["v16"], DEV)
+    bt = torch.from_numpy(inp["block_table"]).to(DEV)
+    kl = torch.from_numpy(inp["kv_seqlens"]).to(DEV)
+    o1, l1 = torch.ops.npu.suffix_decode(q, k, v, bt, kl)
+    o2, l2 = torch.ops.npu.suffix_decode(q, _bnsd(k), _bnsd(v), bt, kl, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+def test_cascade_bnsd_suffix_pool_matches_nhd():
+    import cascade_amd
+    B, H, KVH, P, q16, k16, v16, bt_pre, bt_suf, suf = _cascade_case((6, 64, 8, 640, "long_cut"))
+    q, k, v = (torch_bf16(x, DEV) for x in (q16, k16, v16))
+    btp = torch.from_numpy(bt_pre).to(DEV)
+    bts = torch.from_numpy(bt_suf).to(DEV)
+    plen = torch.tensor([P], dtype=torch.int64, device=DEV)
+    sl = torch.from_numpy(suf).to(DEV)
+    o1, l1 = cascade_amd.ops.cascade_decode(q, k, v, btp, plen, k, v, bts, sl)
+    o2, l2 = cascade_amd.ops.cascade_decode(q, k, v, btp, plen, _bnsd(k), _bnsd(v), bts, sl, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    with pytest.raises(RuntimeError, match="cascade_decode"):
+        cascade_amd.ops.cascade_decode(q, k, v, btp, plen, k, v, bts, sl, 2)

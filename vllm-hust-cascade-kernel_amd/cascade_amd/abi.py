@@ -29,18 +29,20 @@ SIGNATURES = {
     "ck_fa_fp32_stage1": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                  _i64, _i64, _i64, _f32, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
     "ck_suffix_decode_plan": (_int, [_i64, _i64, _i64, _i64, _i64, _p64, _p64]),
-    "ck_suffix_decode": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i64,
-                                _i64, _vp, _vp, _vp, _i64, _vp]),
+    "ck_suffix_decode": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
+                                _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
     "ck_f3_gateup_epilogue": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
     "ck_cascade_decode_plan": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _p64]),
     "ck_cascade_decode": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
-                                 _i64, _i64, _i64, _f32, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
+                                 _i64, _i64, _i64, _i64, _f32, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
     "ck_add_rms_norm_stats": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _int, _i64, _f64, _vp]),
 }
 
 CK_DTYPE_BF16 = 0
 CK_DTYPE_F32 = 1
 CK_DTYPE_F16 = 2
+CK_KV_NHD = 0
+CK_KV_BNSD = 1
 
 _lib = None
 

@@ -22,8 +22,9 @@ def lse_merge_with_lse(o1, o2, lse1, lse2, out_code=0):
     return torch.ops.npu.lse_merge_with_lse(o1, o2, lse1, lse2, out_code)
 
 
-def suffix_decode(query, key, value, block_table, actual_kv_seqlens):
-    return torch.ops.npu.suffix_decode(query, key, value, block_table, actual_kv_seqlens)
+def suffix_decode(query, key, value, block_table, actual_kv_seqlens, kv_layout=0):
+    """kv_layout 0: key/value [numBlocks, 128, KVH, D] (NHD); 1: [numBlocks, KVH, 128, D] (BNSD)."""
+    return torch.ops.npu.suffix_decode(query, key, value, block_table, actual_kv_seqlens, kv_layout)
 
 
 def f3_gateup_epilogue(a, b, workspace=None, out_d=None, mode=1):
@@ -41,16 +42,18 @@ def swiglu_gate_up(a, b):
 
 
 def cascade_decode(query, prefix_key, prefix_value, prefix_block_table, prefix_kv_seqlens,
-                   suffix_key, suffix_value, suffix_block_table, suffix_kv_seqlens):
+                   suffix_key, suffix_value, suffix_block_table, suffix_kv_seqlens, suffix_kv_layout=0):
     """Shared-prefix cascade decode for a batch of B single-token queries, fused.
 
     query [B,H,D] bf16; prefix pages shared by all B sequences (prefix_block_table
     [1, cols], prefix_kv_seqlens int64 [1] on the device); each sequence's suffix
-    through its own suffix_block_table row and suffix_kv_seqlens entry.
+    through its own suffix_block_table row and suffix_kv_seqlens entry; the suffix
+    pool may be NHD (suffix_kv_layout 0, the prefix pool's layout) or BNSD (1).
     Returns (out bf16 [B,H,D], merged LSE fp32 [B*H]).
     """
     return torch.ops.npu.cascade_decode(query, prefix_key, prefix_value, prefix_block_table, prefix_kv_seqlens,
-                                        suffix_key, suffix_value, suffix_block_table, suffix_kv_seqlens)
+                                        suffix_key, suffix_value, suffix_block_table, suffix_kv_seqlens,
+                                        suffix_kv_layout)
 
 
 def cascade_decode_unfused(query, prefix_key, prefix_value, prefix_block_table, prefix_kv_seqlens,

@@ -77,7 +77,8 @@ extern "C" int ck_cascade_decode(const void *q, const void *prefix_k, const void
                                  const int32_t *prefix_block_table, int64_t prefix_bt_cols,
                                  const int64_t *prefix_kv_seqlen, int64_t prefix_num_blocks, const void *suffix_k,
                                  const void *suffix_v, const int32_t *suffix_block_table, int64_t suffix_bt_cols,
-                                 const int64_t *suffix_kv_seqlens, int64_t suffix_num_blocks, int64_t batch,
+                                 const int64_t *suffix_kv_seqlens, int64_t suffix_num_blocks,
+                                 int64_t suffix_kv_layout, int64_t batch,
                                  int64_t num_heads, int64_t kv_heads, int64_t head_dim, int64_t block_size,
                                  float scale, int64_t prefix_cap, int64_t suffix_cap, void *out, float *lse_out,
                                  void *workspace, int64_t workspace_bytes, void *stream) {
@@ -85,6 +86,7 @@ extern "C" int ck_cascade_decode(const void *q, const void *prefix_k, const void
     int rc = cascade_layout(batch, num_heads, kv_heads, head_dim, prefix_cap, suffix_cap, &L);
     if (rc != CK_OK) return rc;
     if (block_size != 128) return CK_E_UNSUPPORTED;
+    if (suffix_kv_layout != CK_KV_NHD && suffix_kv_layout != CK_KV_BNSD) return CK_E_INVALID_ARG;
     if (prefix_bt_cols < 0 || suffix_bt_cols < 0 || prefix_num_blocks < 0 || suffix_num_blocks < 0)
         return CK_E_INVALID_ARG;
     if (prefix_cap > prefix_bt_cols * 128 || suffix_cap > suffix_bt_cols * 128) return CK_E_INVALID_ARG;
@@ -123,7 +125,8 @@ extern "C" int ck_cascade_decode(const void *q, const void *prefix_k, const void
     for (int64_t b0 = 0; b0 < batch; b0 += L.group_batch) {
         const int64_t nb = batch - b0 < L.group_batch ? batch - b0 : L.group_batch;
         rc = ck::suffix_launch_group(q, suffix_k, suffix_v, suffix_block_table, suffix_bt_cols, suffix_kv_seqlens,
-                                     b0, nb, num_heads, kv_heads, suffix_num_blocks, scale, suffix_cap, L.chunks,
+                                     b0, nb, num_heads, kv_heads, suffix_num_blocks, suffix_kv_layout, scale,
+                                     suffix_cap, L.chunks,
                                      o2, l2, sfx_region, &r1, out, lse_out, st);
         if (rc != CK_OK) return rc;
     }

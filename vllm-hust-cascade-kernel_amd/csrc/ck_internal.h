@@ -41,8 +41,8 @@ struct Stage1Result {
 // result of every sequence of the group to final_out/final_lse.
 int suffix_launch_group(const void *q, const void *k, const void *v, const int32_t *block_table, int64_t bt_cols,
                         const int64_t *kv_seqlens, int64_t b0, int64_t nb, int64_t num_heads, int64_t kv_heads,
-                        int64_t num_blocks, float scale, int64_t kv_cap, int64_t chunks, void *out, float *lse,
-                        void *group_ws, const Stage1Result *cascade, void *final_out, float *final_lse,
-                        hipStream_t stream);
+                        int64_t num_blocks, int64_t kv_layout, float scale, int64_t kv_cap, int64_t chunks,
+                        void *out, float *lse, void *group_ws, const Stage1Result *cascade, void *final_out,
+                        float *final_lse, hipStream_t stream);
 
 }  // namespace ck

@@ -20,6 +20,11 @@
 //   windows, crossing sequence boundaries: every workgroup streams the same
 //   number of windows and starts once. Window and length prefix sums are built
 //   per workgroup in LDS from the device-side lengths.
+// * Two paged K/V layouts: NHD [blocks, 128, kv_heads, 128] (the stage-1 pool)
+//   and BNSD [blocks, kv_heads, 128, 128] (the layout the reference's stage-2
+//   op reads, ascend-kernel/README.md:182-183), so a BNSD pool needs no
+//   transposing copy. A page, a token and a kv head are three strides; each
+//   DMA moves four 256-byte token rows of one kv head either way.
 // * K and V rows stream through a 4-stage LDS ring (one window, 32 KB, per
 //   stage) by global->LDS DMA, continuously across sequence boundaries. A
 //   stage's DMA group also carries the block-table entry of the stage three
@@ -85,6 +90,9 @@ struct SuffixArgs {
     int32_t *cw_out;  // [batch + 1] window prefix sums, written by workgroup 0
     int64_t bt_cols;
     int64_t num_blocks;
+    int64_t page_stride;  // elements between pages (both layouts: 128 * kv_heads * 128)
+    int64_t tok_stride;   // between tokens of a page: kv_heads * 128 (NHD) or 128 (BNSD)
+    int64_t head_off;     // between kv heads:          128 (NHD) or 128 * 128 (BNSD)
     int batch;
     int num_heads;
     int kv_heads;
@@ -239,7 +247,6 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
     }
     __syncthreads();
 
-    const int64_t head_stride = (int64_t)a.kv_heads * kD;
     int tot = 0;  // vector-memory operations this wave has issued (wave-uniform)
     // DMA group of window n (cursor cur): the block-table entry of window n + 3
     // (cursor pcur; wave 0), the window's K and V rows, and on the first window
@@ -255,11 +262,12 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
         }
         int page = pgring[n % kPgRing];
         if (page < 0 || (int64_t)page >= a.num_blocks) page = 0;  // rows ignored at use
-        const int64_t tok0 = (int64_t)page * kPage + (cur.k * kWin) % kPage;
+        const int64_t pbase = (int64_t)page * a.page_stride + (int64_t)g * a.head_off + (lane & 15) * 8;
+        const int t0 = (cur.k * kWin) % kPage + (lane >> 4);
 #pragma unroll
         for (int j = 0; j < kKvDmaPerWave / 2; ++j) {
             const int blk = wid * (kKvDmaPerWave / 2) + j;  // 4 token rows per DMA
-            const int64_t off = (tok0 + blk * 4 + (lane >> 4)) * head_stride + g * kD + (lane & 15) * 8;
+            const int64_t off = pbase + (int64_t)(t0 + blk * 4) * a.tok_stride;
             dma16(a.k + off, kb + blk * 1024);
             dma16(a.v + off, vb + blk * 1024);
         }
@@ -711,9 +719,9 @@ int64_t suffix_group_ws_bytes(int64_t nb, int64_t num_heads, int64_t kv_heads, i
 
 int suffix_launch_group(const void *q, const void *k, const void *v, const int32_t *block_table, int64_t bt_cols,
                         const int64_t *kv_seqlens, int64_t b0, int64_t nb, int64_t num_heads, int64_t kv_heads,
-                        int64_t num_blocks, float scale, int64_t kv_cap, int64_t chunks, void *out, float *lse,
-                        void *group_ws, const Stage1Result *cascade, void *final_out, float *final_lse,
-                        hipStream_t stream) {
+                        int64_t num_blocks, int64_t kv_layout, float scale, int64_t kv_cap, int64_t chunks,
+                        void *out, float *lse, void *group_ws, const Stage1Result *cascade, void *final_out,
+                        float *final_lse, hipStream_t stream) {
     const int64_t group = num_heads / kv_heads;
     const int64_t parts = group_parts(num_heads, kv_heads, chunks);
     SuffixArgs a;
@@ -729,6 +737,9 @@ int suffix_launch_group(const void *q, const void *k, const void *v, const int32
     a.cw_out = reinterpret_cast<int32_t *>(a.part_lse + parts);
     a.bt_cols = bt_cols;
     a.num_blocks = num_blocks;
+    a.page_stride = (int64_t)kPage * kv_heads * kD;
+    a.tok_stride = kv_layout == CK_KV_BNSD ? kD : kv_heads * kD;
+    a.head_off = kv_layout == CK_KV_BNSD ? (int64_t)kPage * kD : kD;
     a.batch = (int)nb;
     a.num_heads = (int)num_heads;
     a.kv_heads = (int)kv_heads;
@@ -784,11 +795,12 @@ extern "C" int ck_suffix_decode_plan(int64_t batch, int64_t num_heads, int64_t k
 extern "C" int ck_suffix_decode(const void *q, const void *k, const void *v, const int32_t *block_table,
                                 int64_t bt_cols, const int64_t *kv_seqlens, int64_t batch, int64_t num_heads,
                                 int64_t kv_heads, int64_t head_dim, int64_t num_blocks, int64_t block_size,
-                                float scale, int64_t kv_cap, int64_t num_splits, void *out, float *lse,
-                                void *workspace, int64_t workspace_bytes, void *stream) {
+                                int64_t kv_layout, float scale, int64_t kv_cap, int64_t num_splits, void *out,
+                                float *lse, void *workspace, int64_t workspace_bytes, void *stream) {
     int rc = check_suffix_dims(batch, num_heads, kv_heads, head_dim, kv_cap);
     if (rc != CK_OK) return rc;
     if (block_size != kPage) return CK_E_UNSUPPORTED;
+    if (kv_layout != CK_KV_NHD && kv_layout != CK_KV_BNSD) return CK_E_INVALID_ARG;
     if (bt_cols < 0 || num_blocks < 0 || kv_cap > bt_cols * kPage) return CK_E_INVALID_ARG;
     if (batch == 0) return CK_OK;
     if (!q || !k || !v || !block_table || !kv_seqlens || !out || !lse) return CK_E_NULL_PTR;
@@ -802,7 +814,7 @@ extern "C" int ck_suffix_decode(const void *q, const void *k, const void *v, con
     for (int64_t b0 = 0; b0 < batch; b0 += per_launch) {
         const int64_t nb = batch - b0 < per_launch ? batch - b0 : per_launch;
         rc = suffix_launch_group(q, k, v, block_table, bt_cols, kv_seqlens, b0, nb, num_heads, kv_heads,
-                                 num_blocks, scale, kv_cap, chunks, static_cast<uint16_t *>(out) + b0 * num_heads * kD,
+                                 num_blocks, kv_layout, scale, kv_cap, chunks, static_cast<uint16_t *>(out) + b0 * num_heads * kD,
                                  lse + b0 * num_heads, workspace, nullptr, nullptr, nullptr, st);
         if (rc != CK_OK) return rc;
     }

@@ -233,7 +233,7 @@ std::tuple<at::Tensor, at::Tensor> fa_fp32_stage1_impl(const at::Tensor &query, 
 // ----------------------------------------------------------------------------
 std::tuple<at::Tensor, at::Tensor> suffix_decode_impl(const at::Tensor &query, const at::Tensor &key,
                                                       const at::Tensor &value, const at::Tensor &block_table,
-                                                      const at::Tensor &actual_kv_seqlens) {
+                                                      const at::Tensor &actual_kv_seqlens, int64_t kv_layout) {
     TORCH_CHECK(query.is_contiguous() && key.is_contiguous() && value.is_contiguous() &&
                     block_table.is_contiguous() && actual_kv_seqlens.is_contiguous(),
                 "suffix_decode: all inputs must be contiguous");
@@ -243,14 +243,18 @@ std::tuple<at::Tensor, at::Tensor> suffix_decode_impl(const at::Tensor &query, c
     TORCH_CHECK(block_table.scalar_type() == at::kInt, "suffix_decode: block_table must be int32");
     TORCH_CHECK(actual_kv_seqlens.scalar_type() == at::kLong, "suffix_decode: seqlens must be int64");
     TORCH_CHECK(query.dim() == 3, "suffix_decode: query must be (B, H, D)");
-    TORCH_CHECK(key.dim() == 4 && value.dim() == 4, "suffix_decode: key/value must be (numBlocks, blockSize, KVH, D)");
+    TORCH_CHECK(kv_layout == CK_KV_NHD || kv_layout == CK_KV_BNSD,
+                "suffix_decode: kv_layout must be 0 (NHD) or 1 (BNSD)");
+    TORCH_CHECK(key.dim() == 4 && value.dim() == 4,
+                "suffix_decode: key/value must be (numBlocks, blockSize, KVH, D) or (numBlocks, KVH, blockSize, D)");
     TORCH_CHECK(key.sizes() == value.sizes(), "suffix_decode: key/value shapes must match");
     TORCH_CHECK(block_table.dim() == 2, "suffix_decode: block_table must be (B, cols)");
     TORCH_CHECK(on_device(query) && key.device() == query.device() && value.device() == query.device() &&
                     block_table.device() == query.device() && actual_kv_seqlens.device() == query.device(),
                 "suffix_decode: all tensors must be on the same HIP device");
     const int64_t batch = query.size(0), num_heads = query.size(1), embed = query.size(2);
-    const int64_t kv_heads = key.size(2), block_size = key.size(1);
+    const bool bnsd = kv_layout == CK_KV_BNSD;
+    const int64_t kv_heads = key.size(bnsd ? 1 : 2), block_size = key.size(bnsd ? 2 : 1);
     TORCH_CHECK(actual_kv_seqlens.numel() == batch && block_table.size(0) == batch,
                 "suffix_decode: block_table rows and kv seqlens must have batch entries");
     TORCH_CHECK(embed == 128 && key.size(3) == 128, "suffix_decode: only head dim 128 is supported");
@@ -271,7 +275,7 @@ std::tuple<at::Tensor, at::Tensor> suffix_decode_impl(const at::Tensor &query, c
     const float scale = static_cast<float>(1.0 / std::sqrt(1.0 * embed));
     check_launch(ck_suffix_decode(query.data_ptr(), key.data_ptr(), value.data_ptr(),
                                   block_table.data_ptr<int32_t>(), cols, actual_kv_seqlens.data_ptr<int64_t>(),
-                                  batch, num_heads, kv_heads, embed, key.size(0), block_size, scale, kv_cap,
+                                  batch, num_heads, kv_heads, embed, key.size(0), block_size, kv_layout, scale, kv_cap,
                                   num_splits, out.data_ptr(), lse.data_ptr<float>(),
                                   ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, stream_of(query)),
                  "suffix_decode");
@@ -289,7 +293,7 @@ std::tuple<at::Tensor, at::Tensor> cascade_decode_impl(const at::Tensor &query, 
                                                        const at::Tensor &prefix_kv_seqlens,
                                                        const at::Tensor &suffix_key, const at::Tensor &suffix_value,
                                                        const at::Tensor &suffix_block_table,
-                                                       const at::Tensor &suffix_kv_seqlens) {
+                                                       const at::Tensor &suffix_kv_seqlens, int64_t suffix_kv_layout) {
     for (const at::Tensor *t : {&query, &prefix_key, &prefix_value, &prefix_block_table, &prefix_kv_seqlens,
                                 &suffix_key, &suffix_value, &suffix_block_table, &suffix_kv_seqlens})
         TORCH_CHECK(t->is_contiguous(), "cascade_decode: all inputs must be contiguous");
@@ -304,18 +308,23 @@ std::tuple<at::Tensor, at::Tensor> cascade_decode_impl(const at::Tensor &query, 
     TORCH_CHECK(query.dim() == 3, "cascade_decode: query must be (B, H, D)");
     TORCH_CHECK(prefix_key.dim() == 4 && prefix_key.sizes() == prefix_value.sizes() && suffix_key.dim() == 4 &&
                     suffix_key.sizes() == suffix_value.sizes(),
-                "cascade_decode: key/value must be matching (numBlocks, blockSize, KVH, D)");
+                "cascade_decode: key/value must be matching (numBlocks, blockSize, KVH, D) pools "
+                "(the suffix pool (numBlocks, KVH, blockSize, D) with suffix_kv_layout 1)");
+    TORCH_CHECK(suffix_kv_layout == CK_KV_NHD || suffix_kv_layout == CK_KV_BNSD,
+                "cascade_decode: suffix_kv_layout must be 0 (NHD) or 1 (BNSD)");
+    const bool sfx_bnsd = suffix_kv_layout == CK_KV_BNSD;
     TORCH_CHECK(prefix_block_table.dim() == 2 && prefix_block_table.size(0) >= 1 && prefix_kv_seqlens.numel() == 1,
                 "cascade_decode: the prefix is one request: block_table (1, cols), kv seqlens (1,)");
     const int64_t batch = query.size(0), num_heads = query.size(1), embed = query.size(2);
     const int64_t kv_heads = prefix_key.size(2);
-    TORCH_CHECK(suffix_key.size(2) == kv_heads, "cascade_decode: prefix and suffix pools must have the same kv heads");
+    TORCH_CHECK(suffix_key.size(sfx_bnsd ? 1 : 2) == kv_heads,
+                "cascade_decode: prefix and suffix pools must have the same kv heads");
     TORCH_CHECK(suffix_block_table.dim() == 2 && suffix_block_table.size(0) == batch &&
                     suffix_kv_seqlens.numel() == batch,
                 "cascade_decode: suffix block_table rows and kv seqlens must have batch entries");
     TORCH_CHECK(embed == 128 && prefix_key.size(3) == 128 && suffix_key.size(3) == 128,
                 "cascade_decode: only head dim 128 is supported");
-    TORCH_CHECK(prefix_key.size(1) == 128 && suffix_key.size(1) == 128,
+    TORCH_CHECK(prefix_key.size(1) == 128 && suffix_key.size(sfx_bnsd ? 2 : 1) == 128,
                 "cascade_decode: only paged blockSize 128 is supported");
     TORCH_CHECK(kv_heads > 0 && num_heads % kv_heads == 0, "cascade_decode: numHeads must be a multiple of kvHeads");
     TORCH_CHECK(num_heads / kv_heads <= 8, "cascade_decode: at most 8 query heads per kv head are supported");
@@ -338,7 +347,8 @@ std::tuple<at::Tensor, at::Tensor> cascade_decode_impl(const at::Tensor &query, 
                                    prefix_block_table.data_ptr<int32_t>(), pcols,
                                    prefix_kv_seqlens.data_ptr<int64_t>(), prefix_key.size(0), suffix_key.data_ptr(),
                                    suffix_value.data_ptr(), suffix_block_table.data_ptr<int32_t>(), scols,
-                                   suffix_kv_seqlens.data_ptr<int64_t>(), suffix_key.size(0), batch, num_heads,
+                                   suffix_kv_seqlens.data_ptr<int64_t>(), suffix_key.size(0), suffix_kv_layout,
+                                   batch, num_heads,
                                    kv_heads, embed, 128, scale, prefix_cap, suffix_cap, out.data_ptr(),
                                    lse.data_ptr<float>(), ws.data_ptr(), ws.numel(), stream_of(query)),
                  "cascade_decode");
@@ -467,10 +477,10 @@ TORCH_LIBRARY_FRAGMENT(npu, m) {
     // Additive ops (no reference counterpart in the wheel).
     m.def("lse_merge_with_lse(Tensor o1, Tensor o2, Tensor lse1, Tensor lse2, int out_code=0) -> (Tensor, Tensor)");
     m.def("suffix_decode(Tensor query, Tensor key, Tensor value, Tensor block_table, "
-          "Tensor actual_kv_seqlens) -> (Tensor, Tensor)");
+          "Tensor actual_kv_seqlens, int kv_layout=0) -> (Tensor, Tensor)");
     m.def("cascade_decode(Tensor query, Tensor prefix_key, Tensor prefix_value, Tensor prefix_block_table, "
           "Tensor prefix_kv_seqlens, Tensor suffix_key, Tensor suffix_value, Tensor suffix_block_table, "
-          "Tensor suffix_kv_seqlens) -> (Tensor, Tensor)");
+          "Tensor suffix_kv_seqlens, int suffix_kv_layout=0) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(npu, CUDA, m) {
