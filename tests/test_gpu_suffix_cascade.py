@@ -208,8 +208,9 @@ def test_cascade_fused_matches_unfused():
 
 
 def test_cascade_two_launch_groups():
-    """More sequences than one suffix launch holds (2048): the fused op runs the
-    suffix and epilogue per group; every row still matches the composition."""
+    """More sequences than one suffix launch holds (1024): the fused op runs the
+    suffix and epilogue per group (three here); every row still matches the
+    composition."""
     B, H, KVH, P = 2100, 8, 2, 256
     rng = np.random.default_rng(7)
     suf = rng.integers(0, 80, size=B)

@@ -25,11 +25,14 @@
 //   op reads, ascend-kernel/README.md:182-183), so a BNSD pool needs no
 //   transposing copy. A page, a token and a kv head are three strides; each
 //   DMA moves four 256-byte token rows of one kv head either way.
-// * K and V rows stream through a 4-stage LDS ring (one window, 32 KB, per
-//   stage) by global->LDS DMA, continuously across sequence boundaries. A
-//   stage's DMA group also carries the block-table entry of the stage three
-//   ahead (so page ids never wait on memory inside the loop) and, on the first
-//   window of a sequence, its q rows. Each wave counts its own vector-memory
+// * K and V rows stream through a 2-stage LDS ring (one window, 32 KB, per
+//   stage) by global->LDS DMA, continuously across sequence boundaries. The
+//   ring, prefix sums and scratch take about 78 KB, so two workgroups share a
+//   CU (16 waves): while one waits on its stage the other computes, which
+//   hides more latency than a deeper ring in one workgroup per CU. A stage's
+//   DMA group also carries a block-table entry kStages - 1 windows ahead (so
+//   page ids never wait on memory inside the loop) and, on the first window of
+//   a sequence, its q rows. Each wave counts its own vector-memory
 //   operations (DMAs and output stores) and waits for exactly one stage. Half
 //   the waves issue the next group right after the stage barrier and half after
 //   their compute, so the DMA issue of one half overlaps the other's arithmetic.
@@ -57,12 +60,13 @@ constexpr int kPage = 128;
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kWin = 64;                           // tokens per window (= per ring stage)
-constexpr int kStages = 4;
+constexpr int kStages = 2;
 constexpr int kTileBytes = kWin * kD * 2;          // 16 KB of K (and of V) per stage
 constexpr int kMaxGroup = 8;
 constexpr int kQBytes = kMaxGroup * kD * 2;        // q rows of one (sequence, kv head)
 constexpr int kStageBytes = 2 * kTileBytes + kQBytes;
-constexpr int kMaxBatch = 2048;                    // sequences per launch (prefix sums in LDS)
+constexpr int kMaxBatch = 1024;                    // sequences per launch (prefix sums in LDS)
+constexpr int kBlocksPerCu = 2;                    // resident workgroups per CU the grid is sized for
 constexpr int kPgRing = 8;                         // block-table entries in flight
 constexpr int kKvDmaPerWave = 2 * (kTileBytes / 1024) / kWaves;  // 4
 constexpr float kTau = 8.0f;                       // log2 headroom before the running max moves
@@ -75,7 +79,7 @@ constexpr int kPgOff = kWtotOff + kWaves * 4;                 // int pgring[kPgR
 constexpr int kPwOff = kPgOff + kPgRing * 4;                  // float pw[kWaves][8][kMaxGroup]
 constexpr int kLdsBytes = kPwOff + kWaves * 8 * kMaxGroup * 4;
 static_assert(kPwOff % 16 == 0, "p broadcast rows are read 16 bytes at a time");
-static_assert(kLdsBytes <= 160 * 1024, "fits the CU's LDS");
+static_assert(kLdsBytes * kBlocksPerCu <= 160 * 1024, "kBlocksPerCu workgroups share the CU's LDS");
 
 struct SuffixArgs {
     const uint16_t *q;
@@ -280,24 +284,29 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
     };
 
     // tot right after issuing each group still in flight (oldest first)
-    int gend0 = 0, gend1 = 0, gend2 = 0;
+    int gend[kStages - 1];
+#pragma unroll
+    for (int j = 0; j < kStages - 1; ++j) gend[j] = 0;
+    auto shift_gend = [&]() {
+#pragma unroll
+        for (int j = 0; j + 1 < kStages - 1; ++j) gend[j] = gend[j + 1];
+        gend[kStages - 2] = tot;
+    };
     Cursor ic = cc;
     for (int j = 0; j < kStages - 1; ++j) {
         if (ic.valid) issue(ic, pc, j);
-        gend0 = gend1;
-        gend1 = gend2;
-        gend2 = tot;
+        shift_gend();
         cursor_next(ic, cw, a.batch, w0, w1);
         cursor_next(pc, cw, a.batch, w0, w1);
     }
-    // after the prologue gend0..2 hold groups 0..2
+    // after the prologue gend[] holds groups 0 .. kStages - 2
 
     uint32_t qr[G][8];
     float m[G], thr[G], l[G], acc[G][2];
     int n_done = 0;
     while (cc.valid) {
         // everything issued after this window's group may stay in flight
-        wait_vmcnt_dyn(__builtin_amdgcn_readfirstlane(tot - gend0));
+        wait_vmcnt_dyn(__builtin_amdgcn_readfirstlane(tot - gend[0]));
         __syncthreads();
         const int st = n_done % kStages;
         // the next group goes into the stage consumed last iteration; half the
@@ -411,9 +420,7 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
         }
 
         if (!early && ic.valid) issue(ic, pc, n_done + kStages - 1);
-        gend0 = gend1;
-        gend1 = gend2;
-        gend2 = tot;
+        shift_gend();
         cursor_next(ic, cw, a.batch, w0, w1);
         cursor_next(pc, cw, a.batch, w0, w1);
 
@@ -477,15 +484,69 @@ __device__ __forceinline__ int owner_chunk(int64_t p, int64_t W, int P) {
     return (int)(((p + 1) * P - 1) / W);
 }
 
-// One workgroup per (sequence, kv head): empty suffixes get O = 0, LSE = -inf;
-// a sequence cut by chunk boundaries gets its partials folded; others return.
+// Folds the partials of one query head of a sequence cut by chunk boundaries
+// (chunks ca < cb): the tail slot (1) of chunk ca and the head slot (0) of every
+// later chunk that holds windows, weighted by exp(lse - max). The first kPre
+// chunks' partials are loaded before any is used, so the usual 2-4 chunk case
+// costs one memory round trip; longer runs continue in a loop. The arithmetic
+// (max over all, then a weighted sum in chunk order) does not depend on kPre.
 template <int G>
-__global__ __launch_bounds__(256) void suffix_fixup_kernel(SuffixArgs a) {
+__device__ __forceinline__ void fold_cut(const float *part_o, const float *part_lse, int g, int chunks, int hq,
+                                         int d4, int ca, int cb, int64_t W, float4 &o_out, float &lse_out) {
+    constexpr int kPre = 4;
+    auto pidx = [&](int ch, int sl) { return (((int64_t)g * chunks + ch) * 2 + sl) * G + hq; };
+    // a chunk with no windows (W < P) wrote nothing
+    auto empty_chunk = [&](int ch) { return (int64_t)ch * W / chunks == (int64_t)(ch + 1) * W / chunks; };
+    float pl[kPre];
+    float4 po[kPre];
+    bool ok[kPre];
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+        const int ch = min(ca + j, cb);  // clamped: every load is in bounds
+        ok[j] = ca + j <= cb && (j == 0 || !empty_chunk(ch));
+        const int64_t p = pidx(ch, j == 0 ? 1 : 0);
+        pl[j] = part_lse[p];
+        po[j] = *reinterpret_cast<const float4 *>(part_o + p * kD + 4 * d4);
+    }
+    float mx = pl[0];
+#pragma unroll
+    for (int j = 1; j < kPre; ++j)
+        if (ok[j]) mx = fmaxf(mx, pl[j]);
+    for (int ch = ca + kPre; ch <= cb; ++ch)
+        if (!empty_chunk(ch)) mx = fmaxf(mx, part_lse[pidx(ch, 0)]);
+    const float mu = mx == -INFINITY ? 0.f : mx;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float wsum = 0.f;
+    auto add = [&](float l, const float4 &o) {
+        const float wgt = exp2_fast((l - mu) * kLog2e);
+        acc.x = fmaf(wgt, o.x, acc.x);
+        acc.y = fmaf(wgt, o.y, acc.y);
+        acc.z = fmaf(wgt, o.z, acc.z);
+        acc.w = fmaf(wgt, o.w, acc.w);
+        wsum += wgt;
+    };
+#pragma unroll
+    for (int j = 0; j < kPre; ++j)
+        if (ok[j]) add(pl[j], po[j]);
+    for (int ch = ca + kPre; ch <= cb; ++ch) {
+        if (empty_chunk(ch)) continue;
+        const int64_t p = pidx(ch, 0);
+        add(part_lse[p], *reinterpret_cast<const float4 *>(part_o + p * kD + 4 * d4));
+    }
+    const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
+    o_out = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    lse_out = wsum > 0.f ? mx + __logf(wsum) : -INFINITY;
+}
+
+// One workgroup of 32 G threads per (sequence, kv head): empty suffixes get
+// O = 0, LSE = -inf; a sequence cut by chunk boundaries gets its partials
+// folded; others return.
+template <int G>
+__global__ __launch_bounds__(kMaxGroup * 32) void suffix_fixup_kernel(SuffixArgs a) {
     const int b = blockIdx.x / a.kv_heads;
     const int g = blockIdx.x % a.kv_heads;
     const int hq = threadIdx.x >> 5;
     const int d4 = threadIdx.x & 31;
-    if (hq >= G) return;
     const int64_t beg = a.cw_out[b], end = a.cw_out[b + 1], W = a.cw_out[a.batch];
     const int64_t row = (int64_t)b * a.num_heads + g * G + hq;
     if (end == beg) {
@@ -496,39 +557,25 @@ __global__ __launch_bounds__(256) void suffix_fixup_kernel(SuffixArgs a) {
     const int ca = owner_chunk(beg, W, a.chunks);
     const int cb = owner_chunk(end - 1, W, a.chunks);
     if (ca == cb) return;  // written by the stream kernel
-    auto pidx = [&](int ch, int sl) { return (((int64_t)g * a.chunks + ch) * 2 + sl) * G + hq; };
-    auto empty_chunk = [&](int ch) { return (int64_t)ch * W / a.chunks == (int64_t)(ch + 1) * W / a.chunks; };
-    float mx = a.part_lse[pidx(ca, 1)];
-    for (int ch = ca + 1; ch <= cb; ++ch)
-        if (!empty_chunk(ch)) mx = fmaxf(mx, a.part_lse[pidx(ch, 0)]);
-    const float mu = mx == -INFINITY ? 0.f : mx;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    float wsum = 0.f;
-    for (int ch = ca; ch <= cb; ++ch) {
-        if (empty_chunk(ch)) continue;  // a chunk with no windows (W < P) wrote nothing
-        const int64_t p = pidx(ch, ch == ca ? 1 : 0);
-        const float wgt = exp2_fast((a.part_lse[p] - mu) * kLog2e);
-        const float4 o = *reinterpret_cast<const float4 *>(a.part_o + p * kD + 4 * d4);
-        acc.x = fmaf(wgt, o.x, acc.x);
-        acc.y = fmaf(wgt, o.y, acc.y);
-        acc.z = fmaf(wgt, o.z, acc.z);
-        acc.w = fmaf(wgt, o.w, acc.w);
-        wsum += wgt;
-    }
-    const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
+    float4 o;
+    float l;
+    fold_cut<G>(a.part_o, a.part_lse, g, a.chunks, hq, d4, ca, cb, W, o, l);
     *reinterpret_cast<uint2 *>(a.out + row * kD + 4 * d4) =
-        make_uint2(pack_bf16x2(acc.x * inv, acc.y * inv), pack_bf16x2(acc.z * inv, acc.w * inv));
-    if (d4 == 0) a.lse[row] = wsum > 0.f ? mx + __logf(wsum) : -INFINITY;
+        make_uint2(pack_bf16x2(o.x, o.y), pack_bf16x2(o.z, o.w));
+    if (d4 == 0) a.lse[row] = l;
 }
 
-// Cascade epilogue (fused cascade decode): one workgroup per (sequence, kv head),
-// 32 threads x 4 dims per query head. Folds the stage-1 split partials of the
-// sequence's query token, the suffix result (whole, split partials or empty)
-// and merges the two with the lse_merge arithmetic
+// Cascade epilogue (fused cascade decode): one workgroup of 32 G threads per
+// (sequence, kv head), 32 threads x 4 dims per query head. Folds the stage-1
+// split partials of the sequence's query token, the suffix result (whole, split
+// partials or empty) and merges the two with the lse_merge arithmetic
 //   m = max(l1, l2); w1 = exp(l1 - m); w2 = exp(l2 - m)
 //   out = (o1 w1 + o2 w2) * (1 / (w1 + w2)),  lse = m + log(w1 + w2)
 // (ascend-kernel/csrc/ops/lse_merge/op_kernel/kernel_lse_merge.cpp:237-289);
 // a side at -inf has weight 0, both at -inf give out = 0, lse = -inf.
+// Latency, not bytes, bounds it, so the loads go out in dependency order: the
+// window prefix sums, then every stage-1 partial of the row (up to kPreS
+// splits), then the suffix result those sums locate; the arithmetic waits once.
 struct EpilogueArgs {
     Stage1Result s1;
     const uint16_t *o2;     // bf16 [nb][H][kD] whole-sequence suffix results
@@ -546,61 +593,37 @@ struct EpilogueArgs {
 };
 
 template <int G>
-__global__ __launch_bounds__(256) void cascade_epilogue_kernel(EpilogueArgs e) {
-    constexpr int kBatch = 8;
+__global__ __launch_bounds__(kMaxGroup * 32) void cascade_epilogue_kernel(EpilogueArgs e) {
+    constexpr int kBatch = 8;   // splits folded per rescale step
+    constexpr int kPreS = 16;   // splits loaded up front
     const int bl = blockIdx.x / e.kv_heads;
     const int g = blockIdx.x % e.kv_heads;
     const int hq = threadIdx.x >> 5;
     const int d4 = threadIdx.x & 31;
-    if (hq >= G) return;
     const int h = g * G + hq;
     const int64_t row = (e.b0 + bl) * e.num_heads + h;
+    const int splits = e.s1.splits;
 
-    // ---- stage 1: the prefix result of this query row ---------------------------
-    float l1;
-    float4 o1;
-    if (e.s1.splits <= 1) {
-        o1 = *reinterpret_cast<const float4 *>(e.s1.o + row * kD + 4 * d4);
-        l1 = e.s1.lse[row * 8];
+    const int64_t beg = e.cw[bl], end = e.cw[bl + 1], W = e.cw[e.nb];
+
+    // ---- stage-1 loads: the first kPreS splits of this query row ------------------
+    float ls[kPreS];
+    float4 os[kPreS];
+    if (splits <= 1) {
+        os[0] = *reinterpret_cast<const float4 *>(e.s1.o + row * kD + 4 * d4);
+        ls[0] = e.s1.lse[row * 8];
     } else {
-        float m = -INFINITY, wsum = 0.f;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int s0 = 0; s0 < e.s1.splits; s0 += kBatch) {
-            float ls[kBatch];
-            float4 o[kBatch];
 #pragma unroll
-            for (int j = 0; j < kBatch; ++j) {
-                const int s = s0 + j < e.s1.splits ? s0 + j : e.s1.splits - 1;
-                ls[j] = s0 + j < e.s1.splits ? e.s1.lse[(int64_t)s * e.s1.rows + row] : -INFINITY;
-                o[j] = *reinterpret_cast<const float4 *>(e.s1.o + ((int64_t)s * e.s1.rows + row) * kD + 4 * d4);
-            }
-            float mb = m;
-#pragma unroll
-            for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, ls[j]);
-            const float mu = mb == -INFINITY ? 0.f : mb;
-            const float r = exp2_fast((m - mu) * kLog2e);
-            acc.x *= r; acc.y *= r; acc.z *= r; acc.w *= r;
-            wsum *= r;
-#pragma unroll
-            for (int j = 0; j < kBatch; ++j) {
-                const float wgt = exp2_fast((ls[j] - mu) * kLog2e);
-                acc.x = fmaf(wgt, o[j].x, acc.x);
-                acc.y = fmaf(wgt, o[j].y, acc.y);
-                acc.z = fmaf(wgt, o[j].z, acc.z);
-                acc.w = fmaf(wgt, o[j].w, acc.w);
-                wsum += wgt;
-            }
-            m = mb;
+        for (int j = 0; j < kPreS; ++j) {
+            const int s = j < splits ? j : splits - 1;
+            ls[j] = e.s1.lse[(int64_t)s * e.s1.rows + row];
+            os[j] = *reinterpret_cast<const float4 *>(e.s1.o + ((int64_t)s * e.s1.rows + row) * kD + 4 * d4);
         }
-        const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
-        o1 = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
-        l1 = wsum > 0.f ? m + __logf(wsum) : -INFINITY;
     }
 
     // ---- suffix: empty, whole (bf16 result) or cut by chunk boundaries ------------
     float l2 = -INFINITY;
     float4 o2 = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int64_t beg = e.cw[bl], end = e.cw[bl + 1], W = e.cw[e.nb];
     if (end > beg) {
         const int ca = owner_chunk(beg, W, e.chunks);
         const int cb = owner_chunk(end - 1, W, e.chunks);
@@ -610,31 +633,56 @@ __global__ __launch_bounds__(256) void cascade_epilogue_kernel(EpilogueArgs e) {
             o2 = make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
             l2 = e.lse2[r2];
         } else {
-            auto pidx = [&](int ch, int sl) { return (((int64_t)g * e.chunks + ch) * 2 + sl) * G + hq; };
-            auto empty_chunk = [&](int ch) {
-                return (int64_t)ch * W / e.chunks == (int64_t)(ch + 1) * W / e.chunks;
-            };
-            float mx = e.part_lse[pidx(ca, 1)];
-            for (int ch = ca + 1; ch <= cb; ++ch)
-                if (!empty_chunk(ch)) mx = fmaxf(mx, e.part_lse[pidx(ch, 0)]);
-            const float mu = mx == -INFINITY ? 0.f : mx;
-            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-            float wsum = 0.f;
-            for (int ch = ca; ch <= cb; ++ch) {
-                if (empty_chunk(ch)) continue;
-                const int64_t p = pidx(ch, ch == ca ? 1 : 0);
-                const float wgt = exp2_fast((e.part_lse[p] - mu) * kLog2e);
-                const float4 o = *reinterpret_cast<const float4 *>(e.part_o + p * kD + 4 * d4);
-                acc.x = fmaf(wgt, o.x, acc.x);
-                acc.y = fmaf(wgt, o.y, acc.y);
-                acc.z = fmaf(wgt, o.z, acc.z);
-                acc.w = fmaf(wgt, o.w, acc.w);
+            fold_cut<G>(e.part_o, e.part_lse, g, e.chunks, hq, d4, ca, cb, W, o2, l2);
+        }
+    }
+
+    // ---- stage 1: fold the split partials (online, kBatch splits per step) --------
+    float l1;
+    float4 o1;
+    if (splits <= 1) {
+        o1 = os[0];
+        l1 = ls[0];
+    } else {
+        float m = -INFINITY, wsum = 0.f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        auto step = [&](const float *lb, const float4 *ob, int s0) {
+            float mb = m;
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j)
+                if (s0 + j < splits) mb = fmaxf(mb, lb[j]);
+            const float mu = mb == -INFINITY ? 0.f : mb;
+            const float r = exp2_fast((m - mu) * kLog2e);
+            acc.x *= r; acc.y *= r; acc.z *= r; acc.w *= r;
+            wsum *= r;
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const float wgt = s0 + j < splits ? exp2_fast((lb[j] - mu) * kLog2e) : 0.f;
+                acc.x = fmaf(wgt, ob[j].x, acc.x);
+                acc.y = fmaf(wgt, ob[j].y, acc.y);
+                acc.z = fmaf(wgt, ob[j].z, acc.z);
+                acc.w = fmaf(wgt, ob[j].w, acc.w);
                 wsum += wgt;
             }
-            const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
-            o2 = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
-            l2 = wsum > 0.f ? mx + __logf(wsum) : -INFINITY;
+            m = mb;
+        };
+#pragma unroll
+        for (int s0 = 0; s0 < kPreS; s0 += kBatch)
+            if (s0 < splits) step(ls + s0, os + s0, s0);
+        for (int s0 = kPreS; s0 < splits; s0 += kBatch) {
+            float lb[kBatch];
+            float4 ob[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const int s = s0 + j < splits ? s0 + j : splits - 1;
+                lb[j] = e.s1.lse[(int64_t)s * e.s1.rows + row];
+                ob[j] = *reinterpret_cast<const float4 *>(e.s1.o + ((int64_t)s * e.s1.rows + row) * kD + 4 * d4);
+            }
+            step(lb, ob, s0);
         }
+        const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
+        o1 = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+        l1 = wsum > 0.f ? m + __logf(wsum) : -INFINITY;
     }
 
     // ---- merge --------------------------------------------------------------------
@@ -678,9 +726,9 @@ int launch_suffix(const SuffixArgs &a, bool fixup, const EpilogueArgs *epi, hipS
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
     if (fixup)
-        hipLaunchKernelGGL(suffix_fixup_kernel<G>, dim3((unsigned)(a.batch * a.kv_heads)), dim3(256), 0, st, a);
+        hipLaunchKernelGGL(suffix_fixup_kernel<G>, dim3((unsigned)(a.batch * a.kv_heads)), dim3(32 * G), 0, st, a);
     if (epi)
-        hipLaunchKernelGGL(cascade_epilogue_kernel<G>, dim3((unsigned)(a.batch * a.kv_heads)), dim3(256), 0, st,
+        hipLaunchKernelGGL(cascade_epilogue_kernel<G>, dim3((unsigned)(a.batch * a.kv_heads)), dim3(32 * G), 0, st,
                            *epi);
     CK_RETURN_LAUNCH();
 }
@@ -706,9 +754,9 @@ int64_t suffix_group_batch(int64_t kv_cap) {
     return n < 1 ? 1 : n;
 }
 
-// Workgroups per kv head: about one workgroup per CU over the whole grid.
+// Workgroups per kv head: kBlocksPerCu resident workgroups per CU over the grid.
 int64_t suffix_default_chunks(int64_t kv_heads) {
-    const int64_t p = 256 / kv_heads;
+    const int64_t p = kBlocksPerCu * 256 / kv_heads;
     return p > 0 ? p : 1;
 }
 
