@@ -267,11 +267,6 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
         }
         gp[j] = base + grow * p.k + coff;
     }
-    auto issue = [&](int kt) {
-        CK_LDS char *dst = smem + (kt % kDStages) * kDStageBytes + (kDDmaPerWave * wid) * 1024;
-#pragma unroll
-        for (int j = 0; j < kDDmaPerWave; ++j) dma16(gp[j] + (int64_t)kt * kDBK, dst + j * 1024);
-    };
     f32x16 acc[4][2][2];
 #pragma unroll
     for (int ab = 0; ab < 4; ++ab)
@@ -282,67 +277,78 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[ab][gb][gu][e] = 0.f;
 
-    auto read_frags = [&](int kt, int s, bf16x8 (&wf)[2][2], bf16x8 (&xf)[4]) {
-        const CK_LDS char *xa = smem + (kt % kDStages) * kDStageBytes;
-        const CK_LDS char *wb = xa + kBM * kDRowBytes;
-        const int ch = 2 * s + hh;
-#pragma unroll
-        for (int gb = 0; gb < 2; ++gb) {
-            wf[gb][0] = *reinterpret_cast<const CK_LDS bf16x8 *>(wb + dsw_off(ww * 64 + gb * 32 + l32, ch));
-            wf[gb][1] = *reinterpret_cast<const CK_LDS bf16x8 *>(wb + dsw_off(kBNh + ww * 64 + gb * 32 + l32, ch));
-        }
-#pragma unroll
-        for (int ab = 0; ab < 4; ++ab)
-            xf[ab] = *reinterpret_cast<const CK_LDS bf16x8 *>(xa + dsw_off(wa * 128 + ab * 32 + l32, ch));
+    // DMA j of this wave: K tile `src` into the ring slot of tile `slot`
+    auto dma_one = [&](int slot, int src, int j) {
+        CK_LDS char *dst = smem + (slot % kDStages) * kDStageBytes + (kDDmaPerWave * wid) * 1024;
+        dma16(gp[j] + (int64_t)src * kDBK, dst + j * 1024);
     };
+    static_assert(kDBK == 32 && kDDmaPerWave == 8, "the main loop's issue order assumes two K halves, 8 DMAs");
+    // fragment read r of K half s of the tile in ring slot `slot`: r < 4 -> weight
+    // block (gb, gu) = (r >> 1, r & 1), r >= 4 -> activation block r - 4
+#define CK_GEMM_READ(slot, s, r, WF, XF)                                                                      \
+    do {                                                                                                      \
+        const CK_LDS char *xa_ = smem + ((slot) % kDStages) * kDStageBytes;                                   \
+        const int ch_ = 2 * (s) + hh;                                                                         \
+        if ((r) < 4)                                                                                          \
+            WF[(r) >> 1][(r) & 1] = *reinterpret_cast<const CK_LDS bf16x8 *>(                                  \
+                xa_ + kBM * kDRowBytes + dsw_off(((r) & 1) * kBNh + ww * 64 + ((r) >> 1) * 32 + l32, ch_));   \
+        else                                                                                                  \
+            XF[(r) - 4] = *reinterpret_cast<const CK_LDS bf16x8 *>(                                           \
+                xa_ + dsw_off(wa * 128 + ((r) - 4) * 32 + l32, ch_));                                         \
+    } while (0)
+    // Reads in the order the next half's MFMAs consume them: MFMA 0 needs weight
+    // block 0 and activation block 0 (reads 0 and 4), then 1, 2, 3 one weight block
+    // each, then one activation block every 4 MFMAs, so every wait is partial.
+    constexpr int kReadOrder[8] = {0, 4, 1, 2, 3, 5, 6, 7};
+    // MFMA i of a K half: (ab, gb, gu) = (i >> 2, (i >> 1) & 1, i & 1)
+#define CK_GEMM_MFMA(i, WF, XF)                                                                               \
+    acc[(i) >> 2][((i) >> 1) & 1][(i) & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(                         \
+        WF[((i) >> 1) & 1][(i) & 1], XF[(i) >> 2], acc[(i) >> 2][((i) >> 1) & 1][(i) & 1], 0, 0, 0)
 
-    // prologue: tiles 0 .. kDStages-2 in flight, tile 0 landed everywhere
-    for (int i = 0; i < kDStages - 1; ++i)
-        if (i < ktiles) issue(i);
-    {
-        const int after = min(kDStages - 2, ktiles - 1);  // tiles issued after tile 0
-        if (after >= 3) wait_vmcnt<3 * kDDmaPerWave>();
-        else if (after == 2) wait_vmcnt<2 * kDDmaPerWave>();
-        else if (after == 1) wait_vmcnt<kDDmaPerWave>();
-        else wait_vmcnt<0>();
-    }
+    // prologue: every ring slot in flight (a tile index past the end repeats the
+    // last tile into a slot nothing reads again), tile 0 landed everywhere
+    for (int t = 0; t < kDStages; ++t)
+#pragma unroll
+        for (int j = 0; j < kDDmaPerWave; ++j) dma_one(t, min(t, ktiles - 1), j);
+    wait_vmcnt<(kDStages - 1) * kDDmaPerWave>();
     __syncthreads();
-    bf16x8 wf[2][2][2], xf[2][4];
-    read_frags(0, 0, wf[0], xf[0]);
+    bf16x8 wf0[2][2], xf0[4], wf1[2][2], xf1[4];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) CK_GEMM_READ(0, 0, kReadOrder[r], wf0, xf0);
+    // Each tile: 32 MFMAs in two K halves with the other work placed between
+    // them in a fixed order (sched_barrier fences), so the wave issues its
+    // reads, address arithmetic and DMAs while the matrix pipe is busy:
+    //   half 0: MFMA on (kt, 0) + a read of (kt, 1) after every second MFMA;
+    //   barrier: every read of tile kt is done, tile kt + 1 has landed;
+    //   half 1: MFMA on (kt, 1) + alternately a read of (kt + 1, 0) and one
+    //           of the 8 DMAs of tile kt + kDStages into tile kt's slot.
     for (int kt = 0; kt < ktiles; ++kt) {
-        // the slot of tile kt + kDStages - 1 last held tile kt - 1, which every
-        // wave finished before the barrier at the end of the previous iteration
-        if (kt + kDStages - 1 < ktiles) issue(kt + kDStages - 1);
 #pragma unroll
-        for (int s = 0; s < kDBK / 16; ++s) {
-            if (s + 1 < kDBK / 16) read_frags(kt, s + 1, wf[(s + 1) & 1], xf[(s + 1) & 1]);
-#pragma unroll
-            for (int ab = 0; ab < 4; ++ab)
-#pragma unroll
-                for (int gb = 0; gb < 2; ++gb)
-#pragma unroll
-                    for (int gu = 0; gu < 2; ++gu)
-                        acc[ab][gb][gu] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[s & 1][gb][gu], xf[s & 1][ab],
-                                                                                 acc[ab][gb][gu], 0, 0, 0);
-            if (s + 1 < kDBK / 16) {
-                // one fragment read between every two MFMAs
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-                }
-            }
+        for (int i = 0; i < 16; ++i) {
+            CK_GEMM_MFMA(i, wf0, xf0);
+            if (i % 2 == 0) CK_GEMM_READ(kt, 1, kReadOrder[i / 2], wf1, xf1);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // tile kt + 1 must have landed: the DMAs of the tiles issued after it
-        // (at most kDStages - 2) may still be in flight
-        const int after = min(kDStages - 2, ktiles - 2 - kt);
-        if (after >= 3) wait_vmcnt<3 * kDDmaPerWave>();
-        else if (after == 2) wait_vmcnt<2 * kDDmaPerWave>();
-        else if (after == 1) wait_vmcnt<kDDmaPerWave>();
-        else wait_vmcnt<0>();
+        // tile kt + 1 has landed once at most the groups of tiles kt + 2 and
+        // kt + 3 (issued earlier, real or repeated) remain in flight. In the last
+        // iteration the reads below fetch an unused slot and the DMA repeats the
+        // last tile into tile kt's slot, which nothing reads again.
+        wait_vmcnt<(kDStages - 2) * kDDmaPerWave>();
         __syncthreads();
-        if (kt + 1 < ktiles) read_frags(kt + 1, 0, wf[0], xf[0]);
+        const int tn = min(kt + kDStages, ktiles - 1);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            CK_GEMM_MFMA(i, wf1, xf1);
+            if (i % 2 == 0) CK_GEMM_READ(kt + 1, 0, kReadOrder[i / 2], wf0, xf0);
+            else dma_one(kt, tn, i / 2);  // tile kt's slot: its reads are done
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
+#undef CK_GEMM_READ
+#undef CK_GEMM_MFMA
+    // repeated tiles may still be landing in the ring: drain before the
+    // workgroup's LDS can be handed to another
+    wait_vmcnt<0>();
 
     // ---- epilogue: lane = activation row l32 of block ab; regs 4c..4c+3 of weight
     // block gb = output columns n0 + ww*64 + gb*32 + 8c + 4hh + 0..3 -------------------
