@@ -305,12 +305,18 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
     acc[(i) >> 2][((i) >> 1) & 1][(i) & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(                         \
         WF[((i) >> 1) & 1][(i) & 1], XF[(i) >> 2], acc[(i) >> 2][((i) >> 1) & 1][(i) & 1], 0, 0, 0)
 
-    // prologue: every ring slot in flight (a tile index past the end repeats the
-    // last tile into a slot nothing reads again), tile 0 landed everywhere
+    // DMA schedule: the 8 DMAs of tile t go out in two halves of 4, the first
+    // after the barrier of iteration t - 4 (which frees tile t - 4's slot), the
+    // second in the first K half of iteration t - 3, so the address unit sees
+    // 4 DMAs per wave in every K half instead of 8 in one. A tile index past the
+    // end repeats the last tile into a slot nothing reads again.
+    constexpr int kHalfDma = kDDmaPerWave / 2;
+    // prologue: tiles 0-2 and the first half of tile 3 in flight, tile 0 landed
     for (int t = 0; t < kDStages; ++t)
 #pragma unroll
-        for (int j = 0; j < kDDmaPerWave; ++j) dma_one(t, min(t, ktiles - 1), j);
-    wait_vmcnt<(kDStages - 1) * kDDmaPerWave>();
+        for (int j = 0; j < kDDmaPerWave; ++j)
+            if (t < kDStages - 1 || j < kHalfDma) dma_one(t, min(t, ktiles - 1), j);
+    wait_vmcnt<(kDStages - 2) * kDDmaPerWave + kHalfDma>();
     __syncthreads();
     bf16x8 wf0[2][2], xf0[4], wf1[2][2], xf1[4];
 #pragma unroll
@@ -318,29 +324,32 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
     // Each tile: 32 MFMAs in two K halves with the other work placed between
     // them in a fixed order (sched_barrier fences), so the wave issues its
     // reads, address arithmetic and DMAs while the matrix pipe is busy:
-    //   half 0: MFMA on (kt, 0) + a read of (kt, 1) after every second MFMA;
+    //   half 0: MFMA on (kt, 0) + a read of (kt, 1) after every second MFMA and
+    //           DMAs 4-7 of tile kt + 3 (into tile kt - 1's slot) between;
     //   barrier: every read of tile kt is done, tile kt + 1 has landed;
-    //   half 1: MFMA on (kt, 1) + alternately a read of (kt + 1, 0) and one
-    //           of the 8 DMAs of tile kt + kDStages into tile kt's slot.
+    //   half 1: MFMA on (kt, 1) + a read of (kt + 1, 0) after every second MFMA
+    //           and DMAs 0-3 of tile kt + 4 (into tile kt's slot) between.
     for (int kt = 0; kt < ktiles; ++kt) {
+        const int ta = min(kt + kDStages - 1, ktiles - 1);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             CK_GEMM_MFMA(i, wf0, xf0);
             if (i % 2 == 0) CK_GEMM_READ(kt, 1, kReadOrder[i / 2], wf1, xf1);
+            else if (i % 4 == 1) dma_one(kt + kDStages - 1, ta, kHalfDma + i / 4);
             __builtin_amdgcn_sched_barrier(0);
         }
-        // tile kt + 1 has landed once at most the groups of tiles kt + 2 and
-        // kt + 3 (issued earlier, real or repeated) remain in flight. In the last
-        // iteration the reads below fetch an unused slot and the DMA repeats the
+        // tile kt + 1 has landed once at most the DMAs of tiles kt + 2 and kt + 3
+        // (issued earlier, real or repeated) remain in flight. In the last
+        // iteration the reads below fetch an unused slot and the DMAs repeat the
         // last tile into tile kt's slot, which nothing reads again.
         wait_vmcnt<(kDStages - 2) * kDDmaPerWave>();
         __syncthreads();
-        const int tn = min(kt + kDStages, ktiles - 1);
+        const int tb = min(kt + kDStages, ktiles - 1);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             CK_GEMM_MFMA(i, wf1, xf1);
             if (i % 2 == 0) CK_GEMM_READ(kt + 1, 0, kReadOrder[i / 2], wf0, xf0);
-            else dma_one(kt, tn, i / 2);  // tile kt's slot: its reads are done
+            else if (i % 4 == 1) dma_one(kt + kDStages, tb, i / 4);  // tile kt's slot: its reads are done
             __builtin_amdgcn_sched_barrier(0);
         }
     }
