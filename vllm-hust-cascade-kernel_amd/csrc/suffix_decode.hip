@@ -108,7 +108,26 @@ struct SuffixArgs {
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-#define CK_DPP(x, ctrl) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), ctrl, 0xF, 0xF, false))
+// Every control used below (quad_perm, row_half_mirror, row_ror) reads a lane of
+// the same 16-lane row, so bound_ctrl never applies; setting it lets the
+// compiler fold the move into the consuming add (v_add_f32_dpp).
+#define CK_DPP(x, ctrl) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), ctrl, 0xF, 0xF, true))
+
+// op(x[l], x[l ^ 16]) and op(x[l], x[l ^ 32]) through v_permlane16_swap /
+// v_permlane32_swap: swapping x with itself leaves x[l] in one result and the
+// partner lane's x in the other (a VALU exchange, no LDS round trip).
+__device__ __forceinline__ float max_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // Sum over each aligned group of 8 lanes; every lane of the group gets the total.
 __device__ __forceinline__ float sum8(float x) {
@@ -120,13 +139,11 @@ __device__ __forceinline__ float sum8(float x) {
 // Reduce a value that is constant within each 8-lane group over the 8 groups.
 __device__ __forceinline__ float max_groups(float x) {
     x = fmaxf(x, CK_DPP(x, 0x128));  // row_ror:8, the other group of the 16-lane row
-    x = fmaxf(x, __shfl_xor(x, 16));
-    return fmaxf(x, __shfl_xor(x, 32));
+    return max_xor32(max_xor16(x));
 }
 __device__ __forceinline__ float sum_groups(float x) {
     x += CK_DPP(x, 0x128);
-    x += __shfl_xor(x, 16);
-    return x + __shfl_xor(x, 32);
+    return sum_xor32(sum_xor16(x));
 }
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -302,11 +319,20 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
     // after the prologue gend[] holds groups 0 .. kStages - 2
 
     uint32_t qr[G][8];
-    float m[G], thr[G], l[G], acc[G][2];
+    float m[G], mu[G], thr[G], l[G], acc[G][2];  // mu = m, or 0 while m = -inf
     int n_done = 0;
     while (cc.valid) {
         // everything issued after this window's group may stay in flight
-        wait_vmcnt_dyn(__builtin_amdgcn_readfirstlane(tot - gend[0]));
+        const int after = __builtin_amdgcn_readfirstlane(tot - gend[0]);
+        if constexpr (kStages == 2) {
+            // only the previous segment close's two stores (waves wid < G) can
+            // follow the group of this window: two compares, not a 21-way switch
+            if (after >= 2) wait_vmcnt<2>();
+            else if (after == 1) wait_vmcnt<1>();
+            else wait_vmcnt<0>();
+        } else {
+            wait_vmcnt_dyn(after);
+        }
         __syncthreads();
         const int st = n_done % kStages;
         // the next group goes into the stage consumed last iteration; half the
@@ -332,6 +358,7 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
                 qr[h][0] = q0[0]; qr[h][1] = q0[1]; qr[h][2] = q0[2]; qr[h][3] = q0[3];
                 qr[h][4] = q1[0]; qr[h][5] = q1[1]; qr[h][6] = q1[2]; qr[h][7] = q1[3];
                 m[h] = -INFINITY;
+                mu[h] = 0.f;
                 thr[h] = -INFINITY;
                 l[h] = 0.f;
                 acc[h][0] = 0.f;
@@ -374,6 +401,7 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
                         acc[h][1] *= f;
                         l[h] *= f;
                         m[h] = m_new;
+                        mu[h] = m_new;  // > -inf here
                         thr[h] = m_new + kTau;
                     }
                 }
@@ -383,7 +411,7 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
             for (int h = 0; h < kPwRow; ++h) p[h] = 0.f;
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                p[h] = exp2_fast(s[h] - (m[h] == -INFINITY ? 0.f : m[h]));  // 0 for masked tokens
+                p[h] = exp2_fast(s[h] - mu[h]);  // 0 for masked tokens
                 l[h] += p[h];
             }
             if (c == 0) {
