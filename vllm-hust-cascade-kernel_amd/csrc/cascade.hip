@@ -52,7 +52,7 @@ int cascade_layout(int64_t batch, int64_t num_heads, int64_t kv_heads, int64_t h
     L->s1_splits = s1;
     const int64_t final_bytes = rows * (kD + 8) * (int64_t)sizeof(float);
     L->s1_bytes = align_up(s1 > 1 ? s1_ws : final_bytes);
-    L->chunks = ck::suffix_default_chunks(kv_heads);
+    L->chunks = ck::suffix_default_chunks(num_heads, kv_heads);
     const int64_t per = ck::suffix_group_batch(suffix_cap);
     L->group_batch = batch < per ? batch : per;
     L->sfx_bytes = align_up(ck::suffix_group_ws_bytes(L->group_batch, num_heads, kv_heads, L->chunks));

@@ -23,7 +23,7 @@ int stage1_launch(const void *q, const void *k, const void *v, const int32_t *bl
 // suffix_decode.hip: sequences per launch of the suffix stream kernel, its
 // chunk count and the workspace one launch group needs.
 int64_t suffix_group_batch(int64_t kv_cap);
-int64_t suffix_default_chunks(int64_t kv_heads);
+int64_t suffix_default_chunks(int64_t num_heads, int64_t kv_heads);
 int64_t suffix_group_ws_bytes(int64_t nb, int64_t num_heads, int64_t kv_heads, int64_t chunks);
 
 // Stage-1 result the cascade epilogue folds in, for query token b (row b * H + h).

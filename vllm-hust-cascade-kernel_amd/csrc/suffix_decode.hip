@@ -782,9 +782,14 @@ int64_t suffix_group_batch(int64_t kv_cap) {
     return n < 1 ? 1 : n;
 }
 
-// Workgroups per kv head: kBlocksPerCu resident workgroups per CU over the grid.
-int64_t suffix_default_chunks(int64_t kv_heads) {
-    const int64_t p = kBlocksPerCu * 256 / kv_heads;
+// Workgroups per kv head: the grid holds as many workgroups as can be resident
+// at once. Up to 5 query heads per kv head the stream kernel fits in 128 VGPRs
+// and kBlocksPerCu workgroups share a CU; 6-8 heads need more registers (the
+// per-head accumulators) and run one per CU, where a grid twice that size
+// would queue half its workgroups behind the first half.
+int64_t suffix_default_chunks(int64_t num_heads, int64_t kv_heads) {
+    const int64_t per_cu = num_heads / kv_heads <= 5 ? kBlocksPerCu : 1;
+    const int64_t p = per_cu * 256 / kv_heads;
     return p > 0 ? p : 1;
 }
 
@@ -861,7 +866,7 @@ extern "C" int ck_suffix_decode_plan(int64_t batch, int64_t num_heads, int64_t k
     int rc = check_suffix_dims(batch, num_heads, kv_heads, head_dim, kv_cap);
     if (rc != CK_OK) return rc;
     if (!num_splits || !workspace_bytes) return CK_E_NULL_PTR;
-    const int64_t chunks = suffix_default_chunks(kv_heads);
+    const int64_t chunks = suffix_default_chunks(num_heads, kv_heads);
     const int64_t nb = batch < suffix_group_batch(kv_cap) ? batch : suffix_group_batch(kv_cap);
     *num_splits = chunks;
     *workspace_bytes = batch > 0 ? suffix_group_ws_bytes(nb, num_heads, kv_heads, chunks) : 0;
@@ -880,7 +885,7 @@ extern "C" int ck_suffix_decode(const void *q, const void *k, const void *v, con
     if (bt_cols < 0 || num_blocks < 0 || kv_cap > bt_cols * kPage) return CK_E_INVALID_ARG;
     if (batch == 0) return CK_OK;
     if (!q || !k || !v || !block_table || !kv_seqlens || !out || !lse) return CK_E_NULL_PTR;
-    const int64_t chunks = num_splits > 0 ? num_splits : suffix_default_chunks(kv_heads);
+    const int64_t chunks = num_splits > 0 ? num_splits : suffix_default_chunks(num_heads, kv_heads);
     if (kv_heads * chunks > 0x7FFFFFFF || chunks > (1 << 20)) return CK_E_INVALID_ARG;
     const int64_t per_launch = suffix_group_batch(kv_cap);
     const int64_t nbmax = batch < per_launch ? batch : per_launch;
