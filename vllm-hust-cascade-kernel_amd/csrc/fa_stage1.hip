@@ -21,11 +21,14 @@
 //   query rows 32*(w%4) .. +32 and token half w/4 of every 64-token tile, with
 //   its own online-softmax state; the two halves merge through LDS at the end.
 //   Two waves per SIMD let one wave's softmax VALU overlap the other's MFMAs.
-//   K and V tiles stream into a 4-stage LDS ring (4 x 32 KB) by global->LDS DMA
-//   (global_load_lds, 16 B per lane): no staging registers, three tiles in
-//   flight while one is computed. The split's page ids are read once into LDS,
-//   so no load in the loop depends on another load. Each wave keeps its Q rows
-//   as MFMA operands in registers for the whole kv loop.
+//   K and V tiles stream into a 4-slot LDS ring (4 x 32 KB) by global->LDS DMA
+//   (global_load_lds, 16 B per lane): no staging registers. Tiles go in pairs:
+//   a pair is computed while the next pair lands, with one barrier, one
+//   running-max update and at most one O rescale per pair (the rescale, 64
+//   multiplies per lane, is the largest VALU item of a tile). The split's page
+//   ids are read once into LDS, so no load in the loop depends on another
+//   load. Each wave keeps its Q rows as MFMA operands in registers for the
+//   whole kv loop.
 // * S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (A = K rows from LDS, B = Q); the
 //   accumulator layout puts one query row per lane, so row max / row sum need a
 //   single cross-half exchange. P^T leaves the accumulator directly as the B
@@ -110,13 +113,6 @@ __device__ __forceinline__ bf16x8 pack_p(const f32x16 &s, int base) {
 // Byte offset of row tok, 16-byte chunk c inside a K or V tile (XOR swizzle).
 __device__ __forceinline__ int tile_swz(int tok) { return ((tok & 3) << 2) | ((tok >> 2) & 3); }
 __device__ __forceinline__ int tile_off(int tok, int c) { return tok * (kD * 2) + ((c ^ tile_swz(tok)) << 4); }
-
-__device__ __forceinline__ void wait_tiles(int outstanding) {
-    // at most `outstanding` later tiles (kDmaPerTile DMAs each) may remain in flight
-    if (outstanding >= 2) wait_vmcnt<2 * kDmaPerTile>();
-    else if (outstanding == 1) wait_vmcnt<kDmaPerTile>();
-    else wait_vmcnt<0>();
-}
 
 __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
@@ -233,7 +229,11 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
     float m_run = -INFINITY;
     float l_part = 0.f;  // row sum over the tokens of this lane half
 
-    for (int i = 0; i < kStages - 1 && i < ntiles; ++i) issue_tile(i);
+    // Tiles go in pairs: one barrier, one max update and at most one O rescale
+    // per 128 kv tokens (64 per wave). Pair p (tiles 2p, 2p + 1) is computed
+    // while pair p + 1 lands; the ring's four slots hold exactly those two pairs.
+    static_assert(kStages == 4, "two pairs of tiles in the ring");
+    for (int i = 0; i < 2 && i < ntiles; ++i) issue_tile(i);
 
     // per-lane LDS offsets (loop invariant): K fragment rows of this token half,
     // and the V^T transpose-read addresses. Transpose reads: lane group
@@ -244,52 +244,94 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
     const int tr_row = (lane & 15) >> 2;
     const int tr_e4 = lane & 3;
 
-    for (int i = 0; i < ntiles; ++i) {
-        const int outstanding = min(kStages - 2, ntiles - 1 - i);
-        wait_tiles(outstanding);
-        __syncthreads();
-        const int j0 = kv_lo + i * kTileN;
-        const int nvalid = min(kTileN, kv_hi - j0);
-        const bool page_ok = s_pages[(j0 - kv_lo) / kPage] >= 0;
-        CK_LDS char *kb = smem + (i % kStages) * kStageBytes;
-        CK_LDS char *vb = kb + kTileBytes;
-        if (nvalid < kTileN || !page_ok) {
-            // rows past the sequence end (or of an invalid page) may hold
-            // anything: zero them so 0 * V cannot produce a NaN
-            const int z0 = page_ok ? nvalid : 0;
-            for (int idx = tid; idx < (kTileN - z0) * 16; idx += kThreads) {
-                const int tt = z0 + (idx >> 4), c = idx & 15;
-                *reinterpret_cast<CK_LDS u32x4 *>(kb + tt * 256 + c * 16) = u32x4{0, 0, 0, 0};
-                *reinterpret_cast<CK_LDS u32x4 *>(vb + tt * 256 + c * 16) = u32x4{0, 0, 0, 0};
-            }
-            __syncthreads();
+    // S^T for this wave's token half of the tile in `slot`; tokens past nvalid -> -inf
+    auto qk_tile = [&](int slot, int nvalid, f32x16 &sacc) {
+        const CK_LDS char *kb = smem + slot * kStageBytes;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+            const bf16x8 kf = *reinterpret_cast<const CK_LDS bf16x8 *>(kb + tile_off(ktok, 2 * kk + hh));
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sacc, 0, 0, 0);
         }
-        if (i + kStages - 1 < ntiles) issue_tile(i + kStages - 1);
+        if (nvalid < kTileN) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int tok = th * 32 + (e & 3) + 8 * (e >> 2) + 4 * hh;
+                if (tok >= nvalid) sacc[e] = -INFINITY;
+            }
+        }
+    };
+    // O^T += V^T P^T over this half's 2 k-steps of 16 tokens of the tile in `slot`
+    auto pv_tile = [&](int slot, const f32x16 &pacc) {
+        const CK_LDS char *vb = smem + slot * kStageBytes + kTileBytes;
+#pragma unroll
+        for (int ss = 0; ss < 2; ++ss) {
+            const int s = 2 * th + ss;
+            const bf16x8 pb = pack_p(pacc, ss * 8);
+            const int t1 = 16 * s + 4 * (trG >> 1) + tr_row;  // first read; second is t1 + 8
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const int d = 32 * db + 16 * (trG & 1) + 4 * tr_e4;  // 4 dims this lane addresses
+                const int c = d >> 3, half = (d & 7) * 2;
+                const uint2 lo = lds_read_tr16(vb + tile_off(t1, c) + half);
+                const uint2 hi = lds_read_tr16(vb + tile_off(t1 + 8, c) + half);
+                const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb, oacc[db], 0, 0, 0);
+            }
+        }
+    };
 
-        if (wave_active && th * 32 < nvalid) {
-            f32x16 sacc;
+    for (int i = 0; i < ntiles; i += 2) {
+        const bool two = i + 1 < ntiles;
+        // this pair was issued one pair ago and nothing after it: all landed
+        wait_vmcnt<0>();
+        __syncthreads();
+        int nv[2];
+        bool fill = false;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
-                const bf16x8 kf = *reinterpret_cast<const CK_LDS bf16x8 *>(kb + tile_off(ktok, 2 * kk + hh));
-                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sacc, 0, 0, 0);
-            }
-            // row max of the unscaled scores (mask only on a partial tile); the
-            // scale is > 0, so scaling the max gives the max of the scaled scores
-            float smax = -INFINITY;
-            if (nvalid < kTileN) {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int tok = th * 32 + (e & 3) + 8 * (e >> 2) + 4 * hh;
-                    if (tok >= nvalid) sacc[e] = -INFINITY;
-                    smax = fmaxf(smax, sacc[e]);
+        for (int t = 0; t < 2; ++t) {
+            nv[t] = 0;
+            if (t == 1 && !two) continue;
+            const int j0 = kv_lo + (i + t) * kTileN;
+            nv[t] = min(kTileN, kv_hi - j0);
+            const bool page_ok = s_pages[(j0 - kv_lo) / kPage] >= 0;
+            if (nv[t] < kTileN || !page_ok) {
+                // rows past the sequence end (or of an invalid page) may hold
+                // anything: zero them so 0 * V cannot produce a NaN
+                CK_LDS char *kb = smem + ((i + t) % kStages) * kStageBytes;
+                CK_LDS char *vb = kb + kTileBytes;
+                const int z0 = page_ok ? nv[t] : 0;
+                for (int idx = tid; idx < (kTileN - z0) * 16; idx += kThreads) {
+                    const int tt = z0 + (idx >> 4), c = idx & 15;
+                    *reinterpret_cast<CK_LDS u32x4 *>(kb + tt * 256 + c * 16) = u32x4{0, 0, 0, 0};
+                    *reinterpret_cast<CK_LDS u32x4 *>(vb + tt * 256 + c * 16) = u32x4{0, 0, 0, 0};
                 }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) smax = fmaxf(smax, sacc[e]);
+                fill = true;
             }
-            smax = max_xor32(smax) * a.scale_log2;  // the row's other 16 tokens sit in lane l ^ 32
+        }
+        if (fill) __syncthreads();
+        // the previous pair's slots are free: the pair after this one goes there
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+            if (i + 2 + t < ntiles) issue_tile(i + 2 + t);
+
+        const bool act0 = wave_active && th * 32 < nv[0];
+        const bool act1 = wave_active && th * 32 < nv[1];  // tile i + 1 exists only after a full tile i
+        if (act0) {
+            f32x16 s0, s1;
+            qk_tile(i % kStages, nv[0], s0);
+            if (act1) qk_tile((i + 1) % kStages, nv[1], s1);
+            // row max of the unscaled scores over both tiles; the scale is > 0,
+            // so scaling the max gives the max of the scaled scores
+            float smax = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) smax = fmaxf(smax, s0[e]);
+            if (act1) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) smax = fmaxf(smax, s1[e]);
+            }
+            smax = max_xor32(smax) * a.scale_log2;  // the row's other tokens sit in lane l ^ 32
             const float m_new = fmaxf(m_run, smax);
             const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
             const float dm = exp2_fast(m_run - m_use);
@@ -297,9 +339,17 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
             float ls = 0.f;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const float p = exp2_fast(fmaf(sacc[e], a.scale_log2, -m_use));
-                sacc[e] = p;
+                const float p = exp2_fast(fmaf(s0[e], a.scale_log2, -m_use));
+                s0[e] = p;
                 ls += p;
+            }
+            if (act1) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float p = exp2_fast(fmaf(s1[e], a.scale_log2, -m_use));
+                    s1[e] = p;
+                    ls += p;
+                }
             }
             // the two lane halves hold different tokens of the row: their sums
             // are kept apart and added once after the loop
@@ -312,22 +362,8 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
 #pragma unroll
                     for (int e = 0; e < 16; ++e) oacc[db][e] *= dm;
             }
-            // O^T += V^T P^T over this half's 2 k-steps of 16 tokens
-#pragma unroll
-            for (int ss = 0; ss < 2; ++ss) {
-                const int s = 2 * th + ss;
-                const bf16x8 pb = pack_p(sacc, ss * 8);
-                const int t1 = 16 * s + 4 * (trG >> 1) + tr_row;  // first read; second is t1 + 8
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    const int d = 32 * db + 16 * (trG & 1) + 4 * tr_e4;  // 4 dims this lane addresses
-                    const int c = d >> 3, half = (d & 7) * 2;
-                    const uint2 lo = lds_read_tr16(vb + tile_off(t1, c) + half);
-                    const uint2 hi = lds_read_tr16(vb + tile_off(t1 + 8, c) + half);
-                    const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb, oacc[db], 0, 0, 0);
-                }
-            }
+            pv_tile(i % kStages, s0);
+            if (act1) pv_tile((i + 1) % kStages, s1);
         }
     }
 
