@@ -60,6 +60,12 @@ def test_stage1_plan_and_validation():
 def test_suffix_plan_and_validation():
     s, w = abi.suffix_plan(64, 32, 8, 128, 4096)
     assert s >= 1 and (w == 0) == (s == 1)
+    # the grid holds the workgroups that can be resident at once: two per CU
+    # (256 CUs) up to 5 heads per kv head, one per CU above (more VGPRs)
+    assert abi.suffix_plan(64, 32, 8, 128, 4096)[0] == 2 * 256 // 8
+    assert abi.suffix_plan(64, 40, 8, 128, 4096)[0] == 2 * 256 // 8
+    assert abi.suffix_plan(64, 64, 8, 128, 4096)[0] == 256 // 8
+    assert abi.suffix_plan(64, 8, 1, 128, 4096)[0] == 256
     L = abi.lib()
     out = ctypes.c_int64(0)
     assert L.ck_suffix_decode_plan(4, 64, 4, 128, 100, ctypes.byref(out), ctypes.byref(out)) == -4  # group 16
