@@ -135,6 +135,9 @@ int ck_fa_fp32_stage1(const void *q, const void *k, const void *v, const int32_t
  *   lse          fp32 [batch * num_heads] (compact); a sequence with kv length 0
  *                gets out = 0 and lse = -inf (an empty suffix)
  *   kv_cap       upper bound of kv_seqlens(b), <= bt_cols * 128
+ *   num_splits   workgroups per kv head that share the list of 64-token windows
+ *                (<= 0: the plan's count, as many as are resident at once);
+ *                the plan sizes the workspace for it
  * Same softmax arithmetic as ck_fa_fp32_stage1 (fp32 accumulation).
  * Replaces the closed CANN op npu_fused_infer_attention_score_v2 used as
  * stage 2 (ascend-kernel/README.md:186-197).
