@@ -61,6 +61,16 @@ def test_swiglu_mode1_small_I(M):
     _swiglu_check(bf16_to_np(d), bits_to_f32(a16), bits_to_f32(b16))
 
 
+@pytest.mark.parametrize("K", [64, 96, 128, 160])
+def test_swiglu_short_k_ring(K):
+    """2-5 K tiles of 32: the DMA ring's prologue and last iterations repeat the
+    last tile into ring slots nothing reads again; the result must not see them."""
+    M, I = 40, 128
+    a16, b16 = _inputs(M, K, I, seed=K)
+    d, _ = torch.ops.npu.f3_gateup_epilogue(torch_bf16(a16, DEV), torch_bf16(b16, DEV), None, None, 1)
+    _swiglu_check(bf16_to_np(d), bits_to_f32(a16), bits_to_f32(b16))
+
+
 @pytest.mark.parametrize("M", [1, 16, 256])
 def test_swiglu_config4_shapes(M):
     """K=4096, weight [2*14336, 4096] ~ N(0, 0.02)."""
