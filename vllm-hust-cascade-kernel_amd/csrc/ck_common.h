@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/cascade_kernels.h"
 
 namespace ck {
@@ -124,6 +126,22 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {
     if (b >= full) return b;
     uint32_t per = n / kNumXcd;
     return (b % kNumXcd) * per + b / kNumXcd;
+}
+
+// Raises a kernel's dynamic-LDS limit to `bytes` on the current device, once
+// per device (bit d of `done` records device d). Safe to call from several
+// threads at once: the attribute call is idempotent and the bit is set
+// atomically after it succeeds. Returns CK_OK or the hipError_t.
+inline int ensure_dynamic_lds(const void *fn, int bytes, std::atomic<uint64_t> &done) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return static_cast<int>(e);
+    const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t)1 << dev : 0;
+    if (bit && (done.load(std::memory_order_acquire) & bit)) return CK_OK;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) return static_cast<int>(e);
+    done.fetch_or(bit, std::memory_order_release);
+    return CK_OK;
 }
 
 }  // namespace ck

@@ -599,13 +599,9 @@ int ck::stage1_launch(const void *q, const void *k, const void *v, const int32_t
 
     const int64_t grid = batch * kv_heads * p.mtiles * p.splits;
     if (grid <= 0 || grid > 0x7FFFFFFF) return CK_E_INVALID_ARG;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&stage1_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-        if (e != hipSuccess) return static_cast<int>(e);
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};
+    rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&stage1_kernel), kLdsBytes, lds_set);
+    if (rc != CK_OK) return rc;
     hipLaunchKernelGGL(stage1_kernel, dim3((unsigned)grid), dim3(kThreads), kLdsBytes, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);

@@ -416,23 +416,16 @@ template <int MODE>
 int launch_gemm(const GemmArgs &p, hipStream_t s) {
     const int64_t grid = (int64_t)p.mtiles * p.ntiles;
     if (p.k % kDBK == 0) {
-        static bool attr_set = false;
-        if (!attr_set) {
-            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gateup_dma_kernel<MODE>),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, kDLdsBytes);
-            if (e != hipSuccess) return static_cast<int>(e);
-            attr_set = true;
-        }
+        static std::atomic<uint64_t> lds_set{0};
+        int rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&gateup_dma_kernel<MODE>), kDLdsBytes, lds_set);
+        if (rc != CK_OK) return rc;
         hipLaunchKernelGGL((gateup_dma_kernel<MODE>), dim3((unsigned)grid), dim3(kDThreads), kDLdsBytes, s, p);
         CK_RETURN_LAUNCH();
     }
-    static bool attr_set_g = false;
-    if (!attr_set_g) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gateup_general_kernel<MODE>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kTileBytes);
-        if (e != hipSuccess) return static_cast<int>(e);
-        attr_set_g = true;
-    }
+    static std::atomic<uint64_t> lds_set_g{0};
+    int rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&gateup_general_kernel<MODE>), 2 * kTileBytes,
+                                lds_set_g);
+    if (rc != CK_OK) return rc;
     hipLaunchKernelGGL((gateup_general_kernel<MODE>), dim3((unsigned)grid), dim3(kThreads), 2 * kTileBytes, s, p);
     CK_RETURN_LAUNCH();
 }

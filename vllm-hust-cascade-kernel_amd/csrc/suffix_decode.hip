@@ -741,13 +741,9 @@ int64_t group_parts(int64_t num_heads, int64_t kv_heads, int64_t chunks) {
 
 template <int G>
 int launch_suffix(const SuffixArgs &a, bool fixup, const EpilogueArgs *epi, hipStream_t st) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&suffix_stream_kernel<G>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-        if (e != hipSuccess) return static_cast<int>(e);
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};
+    int rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&suffix_stream_kernel<G>), kLdsBytes, lds_set);
+    if (rc != CK_OK) return rc;
     static_assert((kWaves * G * kD + 2 * kWaves * G) * 4 <= kStageBytes, "exchange fits in a stage");
     hipLaunchKernelGGL(suffix_stream_kernel<G>, dim3((unsigned)(a.kv_heads * a.chunks)), dim3(kThreads), kLdsBytes,
                        st, a);
