@@ -16,7 +16,8 @@ value = end-to-end cascade HBM throughput: algorithmic bytes (q, prefix K/V read
 once, every suffix K/V, block tables, seqlens, final bf16 O and merged LSE) /
 measured time of one fused cascade decode. Inputs are resident in HBM; K/V pools rotate through enough copies
 (>= 2 GiB distinct) that the 256 MB Infinity Cache cannot serve them.
-Each timing loop launches its op back to back on the stream the kernels run on,
+Each timing loop launches its op back to back on the stream the kernels run on
+(the step loop exactly --steps times, each component op at least 100 times),
 with HIP events only at the loop's two ends (an event recorded between two
 kernels delays the second by several microseconds).
 """
@@ -243,8 +244,10 @@ def main():
     ms_step = timed(step, args.steps, args.warmup, warm=False)
     wall = time.perf_counter() - t0
 
-    # component timings over the same number of launches each
-    n = args.steps
+    # component timings: each op over the same number of back-to-back launches, at
+    # least 100, so the start-up gap between the first event and the first kernel
+    # (a host launch latency) is a small share of the loop
+    n = max(args.steps, 100)
     ms = {"cascade": timed(cascade, n, 0), "cascade_unfused": timed(cascade_unfused, n, 0), "gemm": timed(gemm, n, 0),
           "stage1": timed(stage1, n, 0), "suffix": timed(suffix, n, 0), "merge": timed(merge, n, 0),
           "norm0": timed(norm0, n, 0), "norm1": timed(norm1, n, 0)}
