@@ -252,6 +252,22 @@ def main():
           "stage1": timed(stage1, n, 0), "suffix": timed(suffix, n, 0), "merge": timed(merge, n, 0),
           "norm0": timed(norm0, n, 0), "norm1": timed(norm1, n, 0)}
 
+    # decode-sized SwiGLU GEMMs (BASELINE config 4's other M values) over two weight
+    # copies (470 MB together, beyond the Infinity Cache), so the weight stream is
+    # measured from HBM
+    wt_pair = [wt, (torch.randn(2 * GEMM_I, GEMM_K, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)]
+    small_m = {}
+    for mm in (1, 16, 256):
+        a_m = torch.randn(mm, GEMM_K, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        d_m = torch.empty(mm, GEMM_I, device=dev, dtype=torch.bfloat16)
+
+        def gemm_m(i, a_m=a_m, d_m=d_m):
+            torch.ops.npu.f3_gateup_epilogue(a_m, wt_pair[i % 2], None, d_m, 1)
+        t = timed(gemm_m, n, 0)
+        small_m[str(mm)] = {"us": round(t * 1e3, 1),
+                            "weight_gbs": round(2 * GEMM_I * GEMM_K * 2 / (t * 1e-3) / 1e9, 1)}
+    del wt_pair
+
     # HIP-graph batch: one graph holding one fused cascade call per K/V pool copy,
     # replayed back to back (the plugin's graph mode); launch gaps disappear
     side = torch.cuda.Stream()
@@ -331,6 +347,7 @@ def main():
             "mode1_gbs": round((2 * NORM_M * NORM_K * 2 + NORM_K * 2 + NORM_M * 4) / (ms["norm1"] * 1e-3) / 1e9, 1)},
         "swiglu_gemm": {"tflops": round(gemm_tflops, 1), "us": round(ms["gemm"] * 1e3, 1),
                         "pct_of_bf16_peak": round(100.0 * gemm_tflops / BF16_PEAK_TFLOPS, 2)},
+        "swiglu_gemm_small_m": small_m,
         "roofline": {"kernel": dom + " op (" + OP_KERNELS[dom] + ")", "bound": "hbm", "achieved": round(dom_gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
         "roofline_gemm": {"kernel": "f3_gateup_epilogue mode 1", "bound": "mfma", "achieved": round(gemm_tflops, 1),

@@ -93,6 +93,53 @@ def test_swiglu_m4096_sampled_rows():
     _swiglu_check(bf16_to_np(d), bits_to_f32(a16), w["b"], rows)
 
 
+@pytest.mark.parametrize("M,K", [(1, 256), (2, 1024), (31, 512), (32, 768), (33, 512), (8, 320)])
+def test_decode_sized_m(M, K):
+    """M <= 32 with K % 256 == 0 takes the decode-sized kernel (four K quarters per
+    workgroup, partial sums folded in LDS); M = 33 and K = 320 take the DMA ring.
+    Every path must meet the same bound."""
+    I = 256
+    a16, b16 = _inputs(M, K, I, seed=100 + M)
+    d, _ = torch.ops.npu.f3_gateup_epilogue(torch_bf16(a16, DEV), torch_bf16(b16, DEV), None, None, 1)
+    _swiglu_check(bf16_to_np(d), bits_to_f32(a16), bits_to_f32(b16))
+
+
+@pytest.mark.parametrize("mode", [0, 2, 4, 5, 7, 8])
+def test_decode_sized_window_modes(mode):
+    M, K, I = 7, 768, 384
+    a16, b16 = _inputs(M, K, I, seed=200 + mode)
+    a, b = bits_to_f32(a16), bits_to_f32(b16)
+    d, ws = torch.ops.npu.f3_gateup_epilogue(torch_bf16(a16, DEV), torch_bf16(b16, DEV), None, None, mode)
+    c = bf16_to_np(ws)
+    _c_check(c, a, b)
+    dn = bf16_to_np(d)
+    if mode in (0, 5):
+        assert np.array_equal(dn, c[:, :I])
+    elif mode == 4:
+        assert np.array_equal(dn, c[:, I:])
+    elif mode == 8:
+        assert np.all(dn == 0)
+
+
+def test_decode_sized_inplace_d_and_same_c_as_dma_path():
+    """In-place D over the gate half (row stride 2I) on the decode-sized kernel, and
+    its C equal to the DMA ring's C for the same rows (both round the exact fp32
+    sums of the same products; only the summation order differs)."""
+    M, K, I = 12, 1024, 256
+    a16, b16 = _inputs(M, K, I, seed=300)
+    a, b = torch_bf16(a16, DEV), torch_bf16(b16, DEV)
+    _, ws = torch.ops.npu.f3_gateup_epilogue(a, b, None, None, 2)
+    ws2 = torch.empty_like(ws)
+    d0, _ = torch.ops.npu.f3_gateup_epilogue(a, b, ws2, ws2[:, :I], 0)
+    assert d0.stride(0) == 2 * I and torch.equal(ws2, ws)
+    # the same rows inside a 40-row call (DMA ring) give C within one bf16 ulp
+    a40 = torch.cat([a, a, a, a[:4]], 0).contiguous()
+    _, ws40 = torch.ops.npu.f3_gateup_epilogue(a40, b, None, None, 2)
+    diff = (ws40[:M].float() - ws.float()).abs()
+    ulp = ws.float().abs().clamp_min(1e-30) * 2.0 ** -7
+    assert bool((diff <= ulp).all())
+
+
 def _c_check(c, a, b):
     ref = G.gemm_c(a, b)
     exact = G.accumulate(a, b)

@@ -31,6 +31,11 @@
 //   belongs at its LDS slot) so the 32-row fragment reads are bank-conflict
 //   free. The fragments of substep s + 1 are read while the
 //   MFMAs of substep s run, interleaved by scheduling barriers.
+// * Decode-sized kernel (M <= 32, K % 256 == 0): the weight stream bounds the
+//   op, so a workgroup takes 32 gate + 32 up rows (I / 32 workgroups, two per
+//   CU) and its 4 waves each stream a quarter of K from global memory straight
+//   into MFMA operand registers, four 64-deep steps ahead; the partial sums meet
+//   in LDS once.
 // * General kernel (any K % 16 == 0): 8 waves of 128 x (32 + 32), operands
 //   staged global -> registers -> LDS.
 // * Tiles are ordered M-fastest and XCD-aware so the workgroups sharing a
@@ -396,6 +401,121 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
     }
 }
 
+// ---- decode-sized activations (M <= 32) --------------------------------------
+// With few activation rows the op is bound by the weight stream (2I x K bf16),
+// not by MFMA: the 256-row tile above would run I / 128 workgroups (112 at
+// I = 14336) with half their DMAs fetching padding, and the bytes they keep in
+// flight cap the stream near 2.8 TB/s. Here a workgroup takes 32 gate + 32 up
+// weight rows against all activation rows (I / 32 workgroups, two per CU), and
+// each of its 4 waves streams a quarter of K straight from global memory into
+// MFMA operand registers, kSDepth steps ahead; the four partial accumulators
+// meet in LDS once at the end.
+//   Operand layout: per 64-deep K step, lane (row r, half h) loads 64
+//   contiguous bytes of its row, K [64 s + 32 h, +32), as four 16-byte
+//   fragments; MFMA j takes fragment j of both operands, so it contracts the
+//   16 K indices {64 s + 32 h + 8 j + t : h in {0, 1}, t < 8} -- the same K
+//   permutation on both sides, hence the exact product. Activation rows past M
+//   load row M - 1: they feed only output rows that are not stored.
+constexpr int kSThreads = 256;  // 4 waves, wave w reduces K quarter w
+constexpr int kSN = 32;         // gate rows (and as many up rows) per workgroup
+constexpr int kSStep = 64;      // K per pipeline step
+constexpr int kSDepth = 4;      // steps whose loads are in flight per wave
+constexpr int kSMaxM = 32;
+
+template <int MODE>
+__global__ __launch_bounds__(kSThreads) void gateup_skinny_kernel(GemmArgs p) {
+    __shared__ float red[4][2][16][64];  // [wave][gate, up][accumulator register][lane]
+    const int tid = threadIdx.x;
+    const int wid = tid >> 6;
+    const int lane = tid & 63;
+    const int r32 = lane & 31;
+    const int hh = lane >> 5;
+    const int64_t n0 = (int64_t)blockIdx.x * kSN;
+    const int64_t kq = p.k / 4;
+    const int steps = (int)(kq / kSStep);
+    const int64_t koff = wid * kq + 32 * hh;
+    const uint4 *gp = reinterpret_cast<const uint4 *>(p.b + (n0 + r32) * p.k + koff);
+    const uint4 *up = reinterpret_cast<const uint4 *>(p.b + (p.n_half + n0 + r32) * p.k + koff);
+    const int64_t arow = r32 < p.m ? r32 : p.m - 1;
+    const uint4 *xp = reinterpret_cast<const uint4 *>(p.a + arow * p.k + koff);
+    constexpr int kStepVec = kSStep * 2 / 16;  // uint4 per row per step (8)
+
+    uint4 G[kSDepth][4], U[kSDepth][4], X[kSDepth][4];
+    f32x16 accg, accu;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        accg[e] = 0.f;
+        accu[e] = 0.f;
+    }
+#define CK_SKINNY_LOAD(slot, st)                                    \
+    do {                                                            \
+        const int64_t o_ = (int64_t)(st) * kStepVec;                \
+        _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_) {          \
+            G[slot][j_] = gp[o_ + j_];                              \
+            U[slot][j_] = up[o_ + j_];                              \
+            X[slot][j_] = xp[o_ + j_];                              \
+        }                                                           \
+    } while (0)
+#pragma unroll
+    for (int d = 0; d < kSDepth; ++d)
+        if (d < steps) CK_SKINNY_LOAD(d, d);
+    for (int s = 0; s < steps; s += kSDepth) {
+#pragma unroll
+        for (int d = 0; d < kSDepth; ++d) {
+            if (s + d < steps) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const bf16x8 xf = __builtin_bit_cast(bf16x8, X[d][j]);
+                    accg = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, G[d][j]), xf, accg, 0,
+                                                                   0, 0);
+                    accu = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, U[d][j]), xf, accu, 0,
+                                                                   0, 0);
+                }
+                if (s + d + kSDepth < steps) CK_SKINNY_LOAD(d, s + d + kSDepth);
+            }
+        }
+    }
+#undef CK_SKINNY_LOAD
+
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        red[wid][0][e][lane] = accg[e];
+        red[wid][1][e][lane] = accu[e];
+    }
+    __syncthreads();
+    // thread (q = wave, lane): registers 4q .. 4q + 3 of every wave, i.e. output row
+    // (activation) r32 and columns n0 + 8q + 4hh + 0..3 (the 32x32 accumulator layout)
+    const int q = wid;
+    const int64_t gm = r32;
+    if (gm >= p.m) return;
+    float g[4], u[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        g[i] = red[0][0][4 * q + i][lane] + red[1][0][4 * q + i][lane] + red[2][0][4 * q + i][lane] +
+               red[3][0][4 * q + i][lane];
+        u[i] = red[0][1][4 * q + i][lane] + red[1][1][4 * q + i][lane] + red[2][1][4 * q + i][lane] +
+               red[3][1][4 * q + i][lane];
+    }
+    const int64_t col = n0 + 8 * q + 4 * hh;
+    if (MODE == 1) {
+        *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) =
+            make_uint2(pack_bf16x2(silu_mul(g[0], u[0]), silu_mul(g[1], u[1])),
+                       pack_bf16x2(silu_mul(g[2], u[2]), silu_mul(g[3], u[3])));
+    } else {
+        const uint2 gv = make_uint2(pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]));
+        const uint2 uv = make_uint2(pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3]));
+        uint16_t *crow = p.c + gm * (2 * p.n_half);
+        *reinterpret_cast<uint2 *>(crow + col) = gv;
+        *reinterpret_cast<uint2 *>(crow + p.n_half + col) = uv;
+        if (MODE == 0 || MODE == 5)
+            *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = gv;
+        else if (MODE == 4)
+            *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = uv;
+        else if (MODE == 8)
+            *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = make_uint2(0, 0);
+    }
+}
+
 // mode 3: d = workspace[:, :I] (epilogue-only rung), 8 columns per thread.
 __global__ __launch_bounds__(256) void gate_window_copy_kernel(const uint16_t *c, uint16_t *d, int64_t m,
                                                                int64_t n_half, int64_t d_stride) {
@@ -414,6 +534,10 @@ __global__ __launch_bounds__(256) void gate_window_copy_kernel(const uint16_t *c
 
 template <int MODE>
 int launch_gemm(const GemmArgs &p, hipStream_t s) {
+    if (p.m <= kSMaxM && p.k % (4 * kSStep) == 0) {
+        hipLaunchKernelGGL((gateup_skinny_kernel<MODE>), dim3((unsigned)(p.n_half / kSN)), dim3(kSThreads), 0, s, p);
+        CK_RETURN_LAUNCH();
+    }
     const int64_t grid = (int64_t)p.mtiles * p.ntiles;
     if (p.k % kDBK == 0) {
         static std::atomic<uint64_t> lds_set{0};
