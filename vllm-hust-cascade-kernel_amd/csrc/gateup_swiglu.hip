@@ -30,7 +30,10 @@
 //   is XOR-swizzled at 16-byte granularity (the DMA lane fetches the chunk that
 //   belongs at its LDS slot) so the 32-row fragment reads are bank-conflict
 //   free. The fragments of substep s + 1 are read while the
-//   MFMAs of substep s run, interleaved by scheduling barriers.
+//   MFMAs of substep s run, interleaved by scheduling barriers. A half-width
+//   instance (64 gate + 64 up rows, 24 KB stages) runs when the full-width grid
+//   would leave CUs idle (a few m-tiles, e.g. M = 256 at I = 14336: 224
+//   workgroups instead of 112).
 // * Decode-sized kernel (M <= 32, K % 256 == 0): the weight stream bounds the
 //   op, so a workgroup takes 32 gate + 32 up rows (I / 32 workgroups, two per
 //   CU) and its 4 waves each stream a quarter of K from global memory straight
@@ -199,16 +202,27 @@ __global__ __launch_bounds__(kThreads) void gateup_general_kernel(GemmArgs p) {
     }
 }
 
-// ---- main kernel: 4 waves x (128 x 128), DMA-fed 4-stage LDS ring ------------------------
+// ---- main kernel: 4 waves x (128 x 64 WB), DMA-fed 4-stage LDS ring ---------------------
 constexpr int kDThreads = 256;
 constexpr int kDBK = 32;                                  // K per ring stage
 constexpr int kDStages = 4;
 constexpr int kGroupM = 4;   // tile block one XCD runs at once: 4 m-tiles x 8 n-tiles
 constexpr int kGroupN = 8;
 constexpr int kDRowBytes = kDBK * 2;                      // 64 B per staged row
-constexpr int kDStageBytes = (kBM + kBW) * kDRowBytes;    // 32 KB
-constexpr int kDDmaPerWave = kDStageBytes / 1024 / 4;     // 1 KB DMAs per wave per stage (8)
-constexpr int kDLdsBytes = kDStages * kDStageBytes;       // 128 KB
+
+// Workgroup tile of the DMA kernel: 256 activation rows x WB * 64 gate rows (and as
+// many up rows); each wave holds WB 32-row blocks of gate and of up. WB = 2 is the
+// 256 x (128 + 128) tile; WB = 1 halves the weight rows so that a small M (one
+// m-tile) still spreads over twice the workgroups.
+template <int WB>
+struct DmaTile {
+    static constexpr int kNh = 64 * WB;                              // gate rows per workgroup
+    static constexpr int kStageBytes = (kBM + 2 * kNh) * kDRowBytes;  // 32 KB (WB 2) / 24 KB (WB 1)
+    static constexpr int kDmaPerWave = kStageBytes / 1024 / 4;        // 8 / 6
+    static constexpr int kLdsBytes = kDStages * kStageBytes;          // 128 KB / 96 KB
+    static constexpr int kMfmaHalf = 8 * WB;                          // MFMAs per wave per K half
+    static constexpr int kReads = 2 * WB + 4;                         // fragment reads per K half
+};
 
 // Byte offset of 16-byte chunk ch of staged row `row`: 64-byte rows, chunk
 // slot ch ^ f(row) with f(row) = ((row >> 1) ^ (row >> 2)) & 3. A fragment read
@@ -219,8 +233,12 @@ constexpr int kDLdsBytes = kDStages * kDStageBytes;       // 128 KB
 __device__ __forceinline__ int dsw_swz(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
 __device__ __forceinline__ int dsw_off(int row, int ch) { return row * kDRowBytes + ((ch ^ dsw_swz(row)) << 4); }
 
-template <int MODE>
+template <int MODE, int WB>
 __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
+    using T = DmaTile<WB>;
+    constexpr int kBNhW = T::kNh;
+    constexpr int kDStageBytes = T::kStageBytes;
+    constexpr int kDDmaPerWave = T::kDmaPerWave;
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
     CK_LDS char *smem = (CK_LDS char *)smem_raw;
     const int tid = threadIdx.x;
@@ -229,7 +247,7 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
     const int hh = lane >> 5;
     const int l32 = lane & 31;
     const int wa = wid >> 1;  // activation half: rows wa*128 .. +128
-    const int ww = wid & 1;   // weight half: gate rows ww*64 .. +64 (and up)
+    const int ww = wid & 1;   // weight half: gate rows ww*32WB .. +32WB (and up)
 
     const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
     // the 32 workgroups an XCD runs at once (consecutive w after the remap) form
@@ -246,7 +264,7 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
         ni = w / p.mtiles;
     }
     const int64_t m0 = (int64_t)mi * kBM;
-    const int64_t n0 = (int64_t)ni * kBNh;
+    const int64_t n0 = (int64_t)ni * kBNhW;
     const int ktiles = (int)(p.k / kDBK);
 
     // DMA geometry: instruction j of wave w fills staged rows 16*(8w + j) .. +16
@@ -267,16 +285,16 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
             base = p.a;
         } else {
             const int wr = R - kBM;
-            grow = wr < kBNh ? n0 + wr : p.n_half + n0 + (wr - kBNh);
+            grow = wr < kBNhW ? n0 + wr : p.n_half + n0 + (wr - kBNhW);
             base = p.b;
         }
         gp[j] = base + grow * p.k + coff;
     }
-    f32x16 acc[4][2][2];
+    f32x16 acc[4][WB][2];
 #pragma unroll
     for (int ab = 0; ab < 4; ++ab)
 #pragma unroll
-        for (int gb = 0; gb < 2; ++gb)
+        for (int gb = 0; gb < WB; ++gb)
 #pragma unroll
             for (int gu = 0; gu < 2; ++gu)
 #pragma unroll
@@ -287,28 +305,29 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
         CK_LDS char *dst = smem + (slot % kDStages) * kDStageBytes + (kDDmaPerWave * wid) * 1024;
         dma16(gp[j] + (int64_t)src * kDBK, dst + j * 1024);
     };
-    static_assert(kDBK == 32 && kDDmaPerWave == 8, "the main loop's issue order assumes two K halves, 8 DMAs");
-    // fragment read r of K half s of the tile in ring slot `slot`: r < 4 -> weight
-    // block (gb, gu) = (r >> 1, r & 1), r >= 4 -> activation block r - 4
+    static_assert(kDBK == 32 && kDDmaPerWave % 2 == 0 && kDDmaPerWave / 2 <= T::kMfmaHalf / 2,
+                  "two K halves per tile, half the DMAs in each, at most one per MFMA pair");
+    // fragment read r of K half s of the tile in ring slot `slot`: r < 2 WB -> weight
+    // block (gb, gu) = (r >> 1, r & 1), r >= 2 WB -> activation block r - 2 WB
 #define CK_GEMM_READ(slot, s, r, WF, XF)                                                                      \
     do {                                                                                                      \
         const CK_LDS char *xa_ = smem + ((slot) % kDStages) * kDStageBytes;                                   \
         const int ch_ = 2 * (s) + hh;                                                                         \
-        if ((r) < 4)                                                                                          \
+        if ((r) < 2 * WB)                                                                                     \
             WF[(r) >> 1][(r) & 1] = *reinterpret_cast<const CK_LDS bf16x8 *>(                                  \
-                xa_ + kBM * kDRowBytes + dsw_off(((r) & 1) * kBNh + ww * 64 + ((r) >> 1) * 32 + l32, ch_));   \
+                xa_ + kBM * kDRowBytes + dsw_off(((r) & 1) * kBNhW + ww * 32 * WB + ((r) >> 1) * 32 + l32, ch_)); \
         else                                                                                                  \
-            XF[(r) - 4] = *reinterpret_cast<const CK_LDS bf16x8 *>(                                           \
-                xa_ + dsw_off(wa * 128 + ((r) - 4) * 32 + l32, ch_));                                         \
+            XF[(r) - 2 * WB] = *reinterpret_cast<const CK_LDS bf16x8 *>(                                      \
+                xa_ + dsw_off(wa * 128 + ((r) - 2 * WB) * 32 + l32, ch_));                                    \
     } while (0)
     // Reads in the order the next half's MFMAs consume them: MFMA 0 needs weight
-    // block 0 and activation block 0 (reads 0 and 4), then 1, 2, 3 one weight block
-    // each, then one activation block every 4 MFMAs, so every wait is partial.
-    constexpr int kReadOrder[8] = {0, 4, 1, 2, 3, 5, 6, 7};
-    // MFMA i of a K half: (ab, gb, gu) = (i >> 2, (i >> 1) & 1, i & 1)
+    // block 0 and activation block 0, then the other weight blocks one per MFMA,
+    // then one activation block every 2 WB MFMAs, so every wait is partial.
+    constexpr int kReadOrder[8] = {0, 2 * WB, 1, WB == 2 ? 2 : 3, WB == 2 ? 3 : 4, WB == 2 ? 5 : 5, 6, 7};
+    // MFMA i of a K half: (ab, gb, gu) = (i / 2WB, (i / 2) % WB, i % 2)
 #define CK_GEMM_MFMA(i, WF, XF)                                                                               \
-    acc[(i) >> 2][((i) >> 1) & 1][(i) & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(                         \
-        WF[((i) >> 1) & 1][(i) & 1], XF[(i) >> 2], acc[(i) >> 2][((i) >> 1) & 1][(i) & 1], 0, 0, 0)
+    acc[(i) / (2 * WB)][((i) >> 1) % WB][(i) & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(                  \
+        WF[((i) >> 1) % WB][(i) & 1], XF[(i) / (2 * WB)], acc[(i) / (2 * WB)][((i) >> 1) % WB][(i) & 1], 0, 0, 0)
 
     // DMA schedule: the 8 DMAs of tile t go out in two halves of 4, the first
     // after the barrier of iteration t - 4 (which frees tile t - 4's slot), the
@@ -323,9 +342,9 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
             if (t < kDStages - 1 || j < kHalfDma) dma_one(t, min(t, ktiles - 1), j);
     wait_vmcnt<(kDStages - 2) * kDDmaPerWave + kHalfDma>();
     __syncthreads();
-    bf16x8 wf0[2][2], xf0[4], wf1[2][2], xf1[4];
+    bf16x8 wf0[WB][2], xf0[4], wf1[WB][2], xf1[4];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) CK_GEMM_READ(0, 0, kReadOrder[r], wf0, xf0);
+    for (int r = 0; r < T::kReads; ++r) CK_GEMM_READ(0, 0, kReadOrder[r], wf0, xf0);
     // Each tile: 32 MFMAs in two K halves with the other work placed between
     // them in a fixed order (sched_barrier fences), so the wave issues its
     // reads, address arithmetic and DMAs while the matrix pipe is busy:
@@ -337,10 +356,15 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
     for (int kt = 0; kt < ktiles; ++kt) {
         const int ta = min(kt + kDStages - 1, ktiles - 1);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < T::kMfmaHalf; ++i) {
             CK_GEMM_MFMA(i, wf0, xf0);
-            if (i % 2 == 0) CK_GEMM_READ(kt, 1, kReadOrder[i / 2], wf1, xf1);
-            else if (i % 4 == 1) dma_one(kt + kDStages - 1, ta, kHalfDma + i / 4);
+            if (WB == 2) {
+                if (i % 2 == 0) CK_GEMM_READ(kt, 1, kReadOrder[i / 2], wf1, xf1);
+                else if (i % 4 == 1) dma_one(kt + kDStages - 1, ta, kHalfDma + i / 4);
+            } else {
+                if (i < T::kReads) CK_GEMM_READ(kt, 1, kReadOrder[i], wf1, xf1);
+                if (i % 2 == 1 && i / 2 < kHalfDma) dma_one(kt + kDStages - 1, ta, kHalfDma + i / 2);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
         // tile kt + 1 has landed once at most the DMAs of tiles kt + 2 and kt + 3
@@ -351,10 +375,15 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
         __syncthreads();
         const int tb = min(kt + kDStages, ktiles - 1);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < T::kMfmaHalf; ++i) {
             CK_GEMM_MFMA(i, wf1, xf1);
-            if (i % 2 == 0) CK_GEMM_READ(kt + 1, 0, kReadOrder[i / 2], wf0, xf0);
-            else if (i % 4 == 1) dma_one(kt + kDStages, tb, i / 4);  // tile kt's slot: its reads are done
+            if (WB == 2) {
+                if (i % 2 == 0) CK_GEMM_READ(kt + 1, 0, kReadOrder[i / 2], wf0, xf0);
+                else if (i % 4 == 1) dma_one(kt + kDStages, tb, i / 4);  // tile kt's slot: its reads are done
+            } else {
+                if (i < T::kReads) CK_GEMM_READ(kt + 1, 0, kReadOrder[i], wf0, xf0);
+                if (i % 2 == 1 && i / 2 < kHalfDma) dma_one(kt + kDStages, tb, i / 2);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -371,10 +400,10 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
         const int64_t gm = m0 + wa * 128 + ab * 32 + l32;
         if (gm >= p.m) continue;
 #pragma unroll
-        for (int gb = 0; gb < 2; ++gb) {
+        for (int gb = 0; gb < WB; ++gb) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const int64_t col = n0 + ww * 64 + gb * 32 + 8 * c + 4 * hh;
+                const int64_t col = n0 + ww * 32 * WB + gb * 32 + 8 * c + 4 * hh;
                 const f32x16 &G = acc[ab][gb][0];
                 const f32x16 &U = acc[ab][gb][1];
                 const float g0 = G[4 * c + 0], g1 = G[4 * c + 1], g2 = G[4 * c + 2], g3 = G[4 * c + 3];
@@ -532,6 +561,20 @@ __global__ __launch_bounds__(256) void gate_window_copy_kernel(const uint16_t *c
     }
 }
 
+constexpr int64_t kNumCus = 256;  // MI355X
+
+template <int MODE, int WB>
+int launch_dma(GemmArgs p, hipStream_t s) {
+    using T = DmaTile<WB>;
+    p.ntiles = (int)(p.n_half / T::kNh);
+    const int64_t grid = (int64_t)p.mtiles * p.ntiles;
+    static std::atomic<uint64_t> lds_set{0};
+    int rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&gateup_dma_kernel<MODE, WB>), T::kLdsBytes, lds_set);
+    if (rc != CK_OK) return rc;
+    hipLaunchKernelGGL((gateup_dma_kernel<MODE, WB>), dim3((unsigned)grid), dim3(kDThreads), T::kLdsBytes, s, p);
+    CK_RETURN_LAUNCH();
+}
+
 template <int MODE>
 int launch_gemm(const GemmArgs &p, hipStream_t s) {
     if (p.m <= kSMaxM && p.k % (4 * kSStep) == 0) {
@@ -540,11 +583,14 @@ int launch_gemm(const GemmArgs &p, hipStream_t s) {
     }
     const int64_t grid = (int64_t)p.mtiles * p.ntiles;
     if (p.k % kDBK == 0) {
-        static std::atomic<uint64_t> lds_set{0};
-        int rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&gateup_dma_kernel<MODE>), kDLdsBytes, lds_set);
-        if (rc != CK_OK) return rc;
-        hipLaunchKernelGGL((gateup_dma_kernel<MODE>), dim3((unsigned)grid), dim3(kDThreads), kDLdsBytes, s, p);
-        CK_RETURN_LAUNCH();
+        // The half-width tile (WB = 1) does about 3/4 of the full tile's work per
+        // workgroup (its DMA bytes; half the MFMAs) with twice the workgroups: it
+        // wins when it needs fewer than 4/3 as many rounds of resident workgroups
+        // (one per CU), i.e. when the full-width grid leaves CUs idle.
+        const int64_t rounds2 = (grid + kNumCus - 1) / kNumCus;
+        const int64_t rounds1 = (2 * grid + kNumCus - 1) / kNumCus;
+        if (3 * rounds1 < 4 * rounds2) return launch_dma<MODE, 1>(p, s);
+        return launch_dma<MODE, 2>(p, s);
     }
     static std::atomic<uint64_t> lds_set_g{0};
     int rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&gateup_general_kernel<MODE>), 2 * kTileBytes,
