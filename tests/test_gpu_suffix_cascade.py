@@ -222,6 +222,64 @@ def test_cascade_two_launch_groups():
     assert np.all(np.isfinite(lse))
 
 
+def test_cascade_config5_full_size():
+    """BASELINE config 5 at its full size: H = 64, KVH = 8, a 32768-token shared
+    prefix, 256 sequences with geometric suffixes (mean 512, clipped to [1, 4096]),
+    permuted pages; K/V/q generated on the device. Every row: the fused op equals
+    the three-op composition up to the composition's bf16 rounding of the suffix
+    result. Sampled sequences (the longest and shortest suffix and two others):
+    equal to dense attention over the concatenated KV, which is exact row sampling
+    (a sequence's output depends only on its own query, the prefix and its suffix)."""
+    import cascade_amd
+    B, H, KVH, P = 256, 64, 8, 32768
+    rng = np.random.default_rng(55)
+    suf = np.clip(rng.geometric(1 / 512, size=B), 1, 4096).astype(np.int64)
+    nsb = [(int(x) + 127) // 128 for x in suf]
+    nblocks = P // 128 + sum(nsb)
+    perm = rng.permutation(nblocks).astype(np.int32)
+    bt_pre = perm[:P // 128][None, :].copy()
+    bt_suf = np.zeros((B, max(nsb)), dtype=np.int32)
+    off = P // 128
+    for b in range(B):
+        bt_suf[b, :nsb[b]] = perm[off:off + nsb[b]]
+        off += nsb[b]
+    g = torch.Generator(device=DEV).manual_seed(55)
+    k = torch.randn(nblocks, 128, KVH, 128, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(nblocks, 128, KVH, 128, generator=g, device=DEV).to(torch.bfloat16)
+    q = torch.randn(B, H, 128, generator=g, device=DEV).to(torch.bfloat16)
+    args = (q, k, v, torch.from_numpy(bt_pre).to(DEV), torch.tensor([P], dtype=torch.int64, device=DEV),
+            k, v, torch.from_numpy(bt_suf).to(DEV), torch.from_numpy(suf).to(DEV))
+    out, lse = cascade_amd.ops.cascade_decode(*args)
+    ref3 = cascade_amd.ops.cascade_decode_unfused(*args)
+    torch.cuda.synchronize()
+    a, c = out.float(), ref3.float()
+    assert bool(((a - c).abs() <= 2.0 ** -7 * c.abs() + 1e-3).all())
+    assert bool(torch.isfinite(lse).all())
+
+    got = bf16_to_np(out)
+    L = lse.cpu().numpy().reshape(B, H)
+    qf = bits_to_f32(q.cpu().view(torch.int16).numpy().view(np.uint16))
+    pre_pages = torch.from_numpy(bt_pre[0].astype(np.int64)).to(DEV)
+    kp = k[pre_pages].reshape(P, KVH, 128).float().cpu().numpy()
+    vp = v[pre_pages].reshape(P, KVH, 128).float().cpu().numpy()
+    picks = sorted({int(np.argmax(suf)), int(np.argmin(suf)), 17, 200})
+    G = H // KVH
+    for b in picks:
+        pages = torch.from_numpy(bt_suf[b, :nsb[b]].astype(np.int64)).to(DEV)
+        ks = k[pages].reshape(-1, KVH, 128)[:suf[b]].float().cpu().numpy()
+        vs = v[pages].reshape(-1, KVH, 128)[:suf[b]].float().cpu().numpy()
+        kc, vc = np.concatenate([kp, ks]), np.concatenate([vp, vs])
+        for kvh in range(KVH):
+            hs = slice(kvh * G, (kvh + 1) * G)
+            kg = np.repeat(kc[:, kvh:kvh + 1], G, axis=1)
+            vg = np.repeat(vc[:, kvh:kvh + 1], G, axis=1)
+            Od, Ld = A.dense(qf[b:b + 1, hs], kg, vg)
+            err = np.abs(got[b:b + 1, hs] - Od)
+            assert np.all(err <= 2e-3 + 2.0 ** -8 * np.abs(Od)), (b, kvh, err.max())
+            rel = np.abs(L[b, hs] - Ld[0]) / np.maximum(np.abs(Ld[0]), 1.0)
+            assert rel.max() <= 1e-4, (b, kvh, rel.max())
+
+
 def test_cascade_abi_matches_torch_op():
     """ck_cascade_decode through ctypes == torch.ops.npu.cascade_decode (bitwise)."""
     import cascade_amd
