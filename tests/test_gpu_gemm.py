@@ -115,10 +115,12 @@ def test_swiglu_m4096_sampled_rows():
     _swiglu_check(bf16_to_np(d), bits_to_f32(a16), w["b"], rows)
 
 
-@pytest.mark.parametrize("M,K", [(1, 256), (2, 1024), (31, 512), (32, 768), (33, 512), (8, 320)])
+@pytest.mark.parametrize("M,K", [(1, 256), (2, 1024), (16, 512), (17, 256), (31, 512), (32, 768), (33, 512),
+                                 (8, 320)])
 def test_decode_sized_m(M, K):
-    """M <= 32 with K % 256 == 0 takes the decode-sized kernel (four K quarters per
-    workgroup, partial sums folded in LDS); M = 33 and K = 320 take the DMA ring.
+    """M <= 32 with K % 256 == 0 takes a decode-sized kernel (four K quarters per
+    workgroup, partial sums folded in LDS; 16x16x32 MFMA up to M = 16, 32x32x16
+    above); M = 33 and K = 320 take the DMA ring.
     Every path must meet the same bound."""
     I = 256
     a16, b16 = _inputs(M, K, I, seed=100 + M)
@@ -126,9 +128,11 @@ def test_decode_sized_m(M, K):
     _swiglu_check(bf16_to_np(d), bits_to_f32(a16), bits_to_f32(b16))
 
 
+@pytest.mark.parametrize("M", [7, 20])
 @pytest.mark.parametrize("mode", [0, 2, 4, 5, 7, 8])
-def test_decode_sized_window_modes(mode):
-    M, K, I = 7, 768, 384
+def test_decode_sized_window_modes(mode, M):
+    """M <= 16 runs the 16x16x32 variant, 17-32 the 32x32x16 one."""
+    K, I = 768, 384
     a16, b16 = _inputs(M, K, I, seed=200 + mode)
     a, b = bits_to_f32(a16), bits_to_f32(b16)
     d, ws = torch.ops.npu.f3_gateup_epilogue(torch_bf16(a16, DEV), torch_bf16(b16, DEV), None, None, mode)

@@ -38,7 +38,8 @@
 //   op, so a workgroup takes 32 gate + 32 up rows (I / 32 workgroups, two per
 //   CU) and its 4 waves each stream a quarter of K from global memory straight
 //   into MFMA operand registers, four 64-deep steps ahead; the partial sums meet
-//   in LDS once.
+//   in LDS once. Up to M = 16 it runs on 16x16x32 MFMA, whose operand layout
+//   (four lanes per row) halves the address lines per weight byte.
 // * General kernel (any K % 16 == 0): 8 waves of 128 x (32 + 32), operands
 //   staged global -> registers -> LDS.
 // * Tiles are ordered M-fastest and XCD-aware so the workgroups sharing a
@@ -545,6 +546,109 @@ __global__ __launch_bounds__(kSThreads) void gateup_skinny_kernel(GemmArgs p) {
     }
 }
 
+// The same decomposition for M <= 16 on v_mfma_f32_16x16x32_bf16: four lanes per
+// row (K groups of 8) instead of two, so a 16-byte-per-lane load covers 16 rows x
+// 64 B -- 16 address lines per instruction instead of 32, half the address-unit
+// work per weight byte. Per 64-deep K step, lane (row r, group q) loads 32
+// contiguous bytes of its row, K [64 s + 16 q, +16); MFMA j (of 2) takes the j-th
+// 16 bytes of both operands, i.e. K {64 s + 16 q + 8 j + t}, the same permutation
+// on both sides. Each wave holds 4 accumulator tiles (gate/up x 2 blocks of 16 rows).
+constexpr int kS16MaxM = 16;
+
+template <int MODE>
+__global__ __launch_bounds__(kSThreads) void gateup_skinny16_kernel(GemmArgs p) {
+    typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+    __shared__ float red[4][4][4][64];  // [wave][tile: gate b0, gate b1, up b0, up b1][register][lane]
+    const int tid = threadIdx.x;
+    const int wid = tid >> 6;
+    const int lane = tid & 63;
+    const int r16 = lane & 15;
+    const int q4 = lane >> 4;
+    const int64_t n0 = (int64_t)blockIdx.x * kSN;
+    const int64_t kq = p.k / 4;
+    const int steps = (int)(kq / kSStep);
+    const int64_t koff = wid * kq + 16 * q4;
+    const uint4 *wp[4];  // gate rows n0 + 16 b + r16, up rows n_half + n0 + 16 b + r16
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        wp[t] = reinterpret_cast<const uint4 *>(p.b + ((t < 2 ? 0 : p.n_half) + n0 + 16 * (t & 1) + r16) * p.k + koff);
+    const int64_t arow = r16 < p.m ? r16 : p.m - 1;
+    const uint4 *xp = reinterpret_cast<const uint4 *>(p.a + arow * p.k + koff);
+    constexpr int kStepVec = kSStep * 2 / 16;  // uint4 per row per step (8)
+
+    uint4 W[kSDepth][4][2], X[kSDepth][2];
+    f32x4_t acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[t][e] = 0.f;
+#define CK_SKINNY16_LOAD(slot, st)                                          \
+    do {                                                                    \
+        const int64_t o_ = (int64_t)(st) * kStepVec;                        \
+        _Pragma("unroll") for (int j_ = 0; j_ < 2; ++j_) {                  \
+            _Pragma("unroll") for (int t_ = 0; t_ < 4; ++t_) W[slot][t_][j_] = wp[t_][o_ + j_]; \
+            X[slot][j_] = xp[o_ + j_];                                      \
+        }                                                                   \
+    } while (0)
+#pragma unroll
+    for (int d = 0; d < kSDepth; ++d)
+        if (d < steps) CK_SKINNY16_LOAD(d, d);
+    for (int s = 0; s < steps; s += kSDepth) {
+#pragma unroll
+        for (int d = 0; d < kSDepth; ++d) {
+            if (s + d < steps) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const bf16x8 xf = __builtin_bit_cast(bf16x8, X[d][j]);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, W[d][t][j]), xf,
+                                                                         acc[t], 0, 0, 0);
+                }
+                if (s + d + kSDepth < steps) CK_SKINNY16_LOAD(d, s + d + kSDepth);
+            }
+        }
+    }
+#undef CK_SKINNY16_LOAD
+
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[wid][t][e][lane] = acc[t][e];
+    __syncthreads();
+    // thread (wave w, lane): tile pair b = w & 1 (gate b, up b), lanes 32 (w >> 1) .. +32
+    // of it: output row (activation) lane % 16, columns n0 + 16 b + 4 (lane / 16) + 0..3
+    const int b = wid & 1;
+    const int l = 32 * (wid >> 1) + (lane & 31);
+    if (lane >= 32) return;
+    const int64_t gm = l & 15;
+    if (gm >= p.m) return;
+    float g[4], u[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        g[i] = red[0][b][i][l] + red[1][b][i][l] + red[2][b][i][l] + red[3][b][i][l];
+        u[i] = red[0][2 + b][i][l] + red[1][2 + b][i][l] + red[2][2 + b][i][l] + red[3][2 + b][i][l];
+    }
+    const int64_t col = n0 + 16 * b + 4 * (l >> 4);
+    if (MODE == 1) {
+        *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) =
+            make_uint2(pack_bf16x2(silu_mul(g[0], u[0]), silu_mul(g[1], u[1])),
+                       pack_bf16x2(silu_mul(g[2], u[2]), silu_mul(g[3], u[3])));
+    } else {
+        const uint2 gv = make_uint2(pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]));
+        const uint2 uv = make_uint2(pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3]));
+        uint16_t *crow = p.c + gm * (2 * p.n_half);
+        *reinterpret_cast<uint2 *>(crow + col) = gv;
+        *reinterpret_cast<uint2 *>(crow + p.n_half + col) = uv;
+        if (MODE == 0 || MODE == 5)
+            *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = gv;
+        else if (MODE == 4)
+            *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = uv;
+        else if (MODE == 8)
+            *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = make_uint2(0, 0);
+    }
+}
+
 // mode 3: d = workspace[:, :I] (epilogue-only rung), 8 columns per thread.
 __global__ __launch_bounds__(256) void gate_window_copy_kernel(const uint16_t *c, uint16_t *d, int64_t m,
                                                                int64_t n_half, int64_t d_stride) {
@@ -577,6 +681,11 @@ int launch_dma(GemmArgs p, hipStream_t s) {
 
 template <int MODE>
 int launch_gemm(const GemmArgs &p, hipStream_t s) {
+    if (p.m <= kS16MaxM && p.k % (4 * kSStep) == 0) {
+        hipLaunchKernelGGL((gateup_skinny16_kernel<MODE>), dim3((unsigned)(p.n_half / kSN)), dim3(kSThreads), 0, s,
+                           p);
+        CK_RETURN_LAUNCH();
+    }
     if (p.m <= kSMaxM && p.k % (4 * kSStep) == 0) {
         hipLaunchKernelGGL((gateup_skinny_kernel<MODE>), dim3((unsigned)(p.n_half / kSN)), dim3(kSThreads), 0, s, p);
         CK_RETURN_LAUNCH();
