@@ -151,7 +151,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; --gpus %d is not supported "
-              "(the cascade-decode path shards by kv head with no exchange; see DESIGN.md)" % args.gpus,
+              "(the cascade-decode path would shard by kv head, with no exchange between GPUs)" % args.gpus,
               file=sys.stderr)
         sys.exit(2)
     import torch
