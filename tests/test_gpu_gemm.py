@@ -119,8 +119,8 @@ def test_swiglu_m4096_sampled_rows():
                                  (8, 320)])
 def test_decode_sized_m(M, K):
     """M <= 32 with K % 256 == 0 takes a decode-sized kernel (four K quarters per
-    workgroup, partial sums folded in LDS; 16x16x32 MFMA up to M = 16, 32x32x16
-    above); M = 33 and K = 320 take the DMA ring.
+    workgroup, partial sums folded in LDS; one 16-row activation block up to
+    M = 16, two above); M = 33 and K = 320 take the DMA ring.
     Every path must meet the same bound."""
     I = 256
     a16, b16 = _inputs(M, K, I, seed=100 + M)
@@ -131,7 +131,7 @@ def test_decode_sized_m(M, K):
 @pytest.mark.parametrize("M", [7, 20])
 @pytest.mark.parametrize("mode", [0, 2, 4, 5, 7, 8])
 def test_decode_sized_window_modes(mode, M):
-    """M <= 16 runs the 16x16x32 variant, 17-32 the 32x32x16 one."""
+    """The decode-sized kernel with one 16-row activation block (M <= 16) and two."""
     K, I = 768, 384
     a16, b16 = _inputs(M, K, I, seed=200 + mode)
     a, b = bits_to_f32(a16), bits_to_f32(b16)

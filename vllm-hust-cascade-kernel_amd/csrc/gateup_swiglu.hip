@@ -37,9 +37,9 @@
 // * Decode-sized kernel (M <= 32, K % 256 == 0): the weight stream bounds the
 //   op, so a workgroup takes 32 gate + 32 up rows (I / 32 workgroups, two per
 //   CU) and its 4 waves each stream a quarter of K from global memory straight
-//   into MFMA operand registers, four 64-deep steps ahead; the partial sums meet
-//   in LDS once. Up to M = 16 it runs on 16x16x32 MFMA, whose operand layout
-//   (four lanes per row) halves the address lines per weight byte.
+//   into MFMA operand registers, several 64-deep steps ahead; the partial sums
+//   meet in LDS once. It runs on 16x16x32 MFMA, whose operand layout (four lanes
+//   per row) needs half the address lines per weight byte of the 32x32 one.
 // * General kernel (any K % 16 == 0): 8 waves of 128 x (32 + 32), operands
 //   staged global -> registers -> LDS.
 // * Tiles are ordered M-fastest and XCD-aware so the workgroups sharing a
@@ -438,127 +438,29 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
 // flight cap the stream near 2.8 TB/s. Here a workgroup takes 32 gate + 32 up
 // weight rows against all activation rows (I / 32 workgroups, two per CU), and
 // each of its 4 waves streams a quarter of K straight from global memory into
-// MFMA operand registers, kSDepth steps ahead; the four partial accumulators
+// MFMA operand registers, several steps ahead; the four partial accumulators
 // meet in LDS once at the end.
-//   Operand layout: per 64-deep K step, lane (row r, half h) loads 64
-//   contiguous bytes of its row, K [64 s + 32 h, +32), as four 16-byte
-//   fragments; MFMA j takes fragment j of both operands, so it contracts the
-//   16 K indices {64 s + 32 h + 8 j + t : h in {0, 1}, t < 8} -- the same K
-//   permutation on both sides, hence the exact product. Activation rows past M
-//   load row M - 1: they feed only output rows that are not stored.
+//   On v_mfma_f32_16x16x32_bf16 four lanes share a row (K groups of 8), so a
+//   16-byte-per-lane load covers 16 rows x 64 B: 16 address lines per
+//   instruction, half what the 32x32 layout (two lanes per row) needs per weight
+//   byte. Per 64-deep K step, lane (row r, group q) loads 32 contiguous bytes of
+//   its row, K [64 s + 16 q, +16); MFMA j (of 2) takes the j-th 16 bytes of both
+//   operands, i.e. K {64 s + 16 q + 8 j + t}, the same permutation on both sides,
+//   hence the exact product. Each wave holds 4 weight tiles (gate/up x 2 blocks of
+//   16 rows) per 16-row activation block (NB = 1 up to M = 16, 2 up to M = 32).
+//   Activation rows past M load row M - 1: they feed only output rows that are
+//   not stored.
 constexpr int kSThreads = 256;  // 4 waves, wave w reduces K quarter w
 constexpr int kSN = 32;         // gate rows (and as many up rows) per workgroup
 constexpr int kSStep = 64;      // K per pipeline step
-constexpr int kSDepth = 4;      // steps whose loads are in flight per wave
+constexpr int kSDepth = 4;      // steps whose loads are in flight per wave (NB = 1)
 constexpr int kSMaxM = 32;
 
-template <int MODE>
-__global__ __launch_bounds__(kSThreads) void gateup_skinny_kernel(GemmArgs p) {
-    __shared__ float red[4][2][16][64];  // [wave][gate, up][accumulator register][lane]
-    const int tid = threadIdx.x;
-    const int wid = tid >> 6;
-    const int lane = tid & 63;
-    const int r32 = lane & 31;
-    const int hh = lane >> 5;
-    const int64_t n0 = (int64_t)blockIdx.x * kSN;
-    const int64_t kq = p.k / 4;
-    const int steps = (int)(kq / kSStep);
-    const int64_t koff = wid * kq + 32 * hh;
-    const uint4 *gp = reinterpret_cast<const uint4 *>(p.b + (n0 + r32) * p.k + koff);
-    const uint4 *up = reinterpret_cast<const uint4 *>(p.b + (p.n_half + n0 + r32) * p.k + koff);
-    const int64_t arow = r32 < p.m ? r32 : p.m - 1;
-    const uint4 *xp = reinterpret_cast<const uint4 *>(p.a + arow * p.k + koff);
-    constexpr int kStepVec = kSStep * 2 / 16;  // uint4 per row per step (8)
-
-    uint4 G[kSDepth][4], U[kSDepth][4], X[kSDepth][4];
-    f32x16 accg, accu;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        accg[e] = 0.f;
-        accu[e] = 0.f;
-    }
-#define CK_SKINNY_LOAD(slot, st)                                    \
-    do {                                                            \
-        const int64_t o_ = (int64_t)(st) * kStepVec;                \
-        _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_) {          \
-            G[slot][j_] = gp[o_ + j_];                              \
-            U[slot][j_] = up[o_ + j_];                              \
-            X[slot][j_] = xp[o_ + j_];                              \
-        }                                                           \
-    } while (0)
-#pragma unroll
-    for (int d = 0; d < kSDepth; ++d)
-        if (d < steps) CK_SKINNY_LOAD(d, d);
-    for (int s = 0; s < steps; s += kSDepth) {
-#pragma unroll
-        for (int d = 0; d < kSDepth; ++d) {
-            if (s + d < steps) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const bf16x8 xf = __builtin_bit_cast(bf16x8, X[d][j]);
-                    accg = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, G[d][j]), xf, accg, 0,
-                                                                   0, 0);
-                    accu = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, U[d][j]), xf, accu, 0,
-                                                                   0, 0);
-                }
-                if (s + d + kSDepth < steps) CK_SKINNY_LOAD(d, s + d + kSDepth);
-            }
-        }
-    }
-#undef CK_SKINNY_LOAD
-
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        red[wid][0][e][lane] = accg[e];
-        red[wid][1][e][lane] = accu[e];
-    }
-    __syncthreads();
-    // thread (q = wave, lane): registers 4q .. 4q + 3 of every wave, i.e. output row
-    // (activation) r32 and columns n0 + 8q + 4hh + 0..3 (the 32x32 accumulator layout)
-    const int q = wid;
-    const int64_t gm = r32;
-    if (gm >= p.m) return;
-    float g[4], u[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        g[i] = red[0][0][4 * q + i][lane] + red[1][0][4 * q + i][lane] + red[2][0][4 * q + i][lane] +
-               red[3][0][4 * q + i][lane];
-        u[i] = red[0][1][4 * q + i][lane] + red[1][1][4 * q + i][lane] + red[2][1][4 * q + i][lane] +
-               red[3][1][4 * q + i][lane];
-    }
-    const int64_t col = n0 + 8 * q + 4 * hh;
-    if (MODE == 1) {
-        *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) =
-            make_uint2(pack_bf16x2(silu_mul(g[0], u[0]), silu_mul(g[1], u[1])),
-                       pack_bf16x2(silu_mul(g[2], u[2]), silu_mul(g[3], u[3])));
-    } else {
-        const uint2 gv = make_uint2(pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]));
-        const uint2 uv = make_uint2(pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3]));
-        uint16_t *crow = p.c + gm * (2 * p.n_half);
-        *reinterpret_cast<uint2 *>(crow + col) = gv;
-        *reinterpret_cast<uint2 *>(crow + p.n_half + col) = uv;
-        if (MODE == 0 || MODE == 5)
-            *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = gv;
-        else if (MODE == 4)
-            *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = uv;
-        else if (MODE == 8)
-            *reinterpret_cast<uint2 *>(p.d + gm * p.d_stride + col) = make_uint2(0, 0);
-    }
-}
-
-// The same decomposition for M <= 16 on v_mfma_f32_16x16x32_bf16: four lanes per
-// row (K groups of 8) instead of two, so a 16-byte-per-lane load covers 16 rows x
-// 64 B -- 16 address lines per instruction instead of 32, half the address-unit
-// work per weight byte. Per 64-deep K step, lane (row r, group q) loads 32
-// contiguous bytes of its row, K [64 s + 16 q, +16); MFMA j (of 2) takes the j-th
-// 16 bytes of both operands, i.e. K {64 s + 16 q + 8 j + t}, the same permutation
-// on both sides. Each wave holds 4 accumulator tiles (gate/up x 2 blocks of 16 rows).
-constexpr int kS16MaxM = 16;
-
-template <int MODE>
+template <int MODE, int NB>  // NB = 16-row activation blocks (M <= 16 NB)
 __global__ __launch_bounds__(kSThreads) void gateup_skinny16_kernel(GemmArgs p) {
     typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
-    __shared__ float red[4][4][4][64];  // [wave][tile: gate b0, gate b1, up b0, up b1][register][lane]
+    // [wave][weight tile: gate b0, gate b1, up b0, up b1][activation block][register][lane]
+    __shared__ float red[4][4][NB][4][64];
     const int tid = threadIdx.x;
     const int wid = tid >> 6;
     const int lane = tid & 63;
@@ -572,40 +474,49 @@ __global__ __launch_bounds__(kSThreads) void gateup_skinny16_kernel(GemmArgs p) 
 #pragma unroll
     for (int t = 0; t < 4; ++t)
         wp[t] = reinterpret_cast<const uint4 *>(p.b + ((t < 2 ? 0 : p.n_half) + n0 + 16 * (t & 1) + r16) * p.k + koff);
-    const int64_t arow = r16 < p.m ? r16 : p.m - 1;
-    const uint4 *xp = reinterpret_cast<const uint4 *>(p.a + arow * p.k + koff);
+    const uint4 *xp[NB];
+#pragma unroll
+    for (int ab = 0; ab < NB; ++ab) {
+        const int64_t arow = 16 * ab + r16 < p.m ? 16 * ab + r16 : p.m - 1;
+        xp[ab] = reinterpret_cast<const uint4 *>(p.a + arow * p.k + koff);
+    }
     constexpr int kStepVec = kSStep * 2 / 16;  // uint4 per row per step (8)
+    constexpr int kDepth = NB == 1 ? kSDepth : 3;  // registers: 48 per step at NB = 2
 
-    uint4 W[kSDepth][4][2], X[kSDepth][2];
-    f32x4_t acc[4];
+    uint4 W[kDepth][4][2], X[kDepth][NB][2];
+    f32x4_t acc[4][NB];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[t][e] = 0.f;
+        for (int ab = 0; ab < NB; ++ab)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[t][ab][e] = 0.f;
 #define CK_SKINNY16_LOAD(slot, st)                                          \
     do {                                                                    \
         const int64_t o_ = (int64_t)(st) * kStepVec;                        \
         _Pragma("unroll") for (int j_ = 0; j_ < 2; ++j_) {                  \
             _Pragma("unroll") for (int t_ = 0; t_ < 4; ++t_) W[slot][t_][j_] = wp[t_][o_ + j_]; \
-            X[slot][j_] = xp[o_ + j_];                                      \
+            _Pragma("unroll") for (int b_ = 0; b_ < NB; ++b_) X[slot][b_][j_] = xp[b_][o_ + j_]; \
         }                                                                   \
     } while (0)
 #pragma unroll
-    for (int d = 0; d < kSDepth; ++d)
+    for (int d = 0; d < kDepth; ++d)
         if (d < steps) CK_SKINNY16_LOAD(d, d);
-    for (int s = 0; s < steps; s += kSDepth) {
+    for (int s = 0; s < steps; s += kDepth) {
 #pragma unroll
-        for (int d = 0; d < kSDepth; ++d) {
+        for (int d = 0; d < kDepth; ++d) {
             if (s + d < steps) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const bf16x8 xf = __builtin_bit_cast(bf16x8, X[d][j]);
+                for (int j = 0; j < 2; ++j)
 #pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, W[d][t][j]), xf,
-                                                                         acc[t], 0, 0, 0);
-                }
-                if (s + d + kSDepth < steps) CK_SKINNY16_LOAD(d, s + d + kSDepth);
+                    for (int ab = 0; ab < NB; ++ab) {
+                        const bf16x8 xf = __builtin_bit_cast(bf16x8, X[d][ab][j]);
+#pragma unroll
+                        for (int t = 0; t < 4; ++t)
+                            acc[t][ab] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                __builtin_bit_cast(bf16x8, W[d][t][j]), xf, acc[t][ab], 0, 0, 0);
+                    }
+                if (s + d + kDepth < steps) CK_SKINNY16_LOAD(d, s + d + kDepth);
             }
         }
     }
@@ -614,20 +525,23 @@ __global__ __launch_bounds__(kSThreads) void gateup_skinny16_kernel(GemmArgs p) 
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) red[wid][t][e][lane] = acc[t][e];
+        for (int ab = 0; ab < NB; ++ab)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) red[wid][t][ab][e][lane] = acc[t][ab][e];
     __syncthreads();
-    // thread (wave w, lane): tile pair b = w & 1 (gate b, up b), lanes 32 (w >> 1) .. +32
-    // of it: output row (activation) lane % 16, columns n0 + 16 b + 4 (lane / 16) + 0..3
-    const int b = wid & 1;
-    const int l = 32 * (wid >> 1) + (lane & 31);
-    if (lane >= 32) return;
-    const int64_t gm = l & 15;
+    // thread -> (weight tile pair b: gate b and up b, activation block ab, accumulator
+    // lane l): output row 16 ab + l % 16, columns n0 + 16 b + 4 (l / 16) + 0..3
+    if (tid >= 2 * NB * 64) return;
+    const int b = tid / (NB * 64);
+    const int ab = (tid / 64) % NB;
+    const int l = tid & 63;
+    const int64_t gm = 16 * ab + (l & 15);
     if (gm >= p.m) return;
     float g[4], u[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        g[i] = red[0][b][i][l] + red[1][b][i][l] + red[2][b][i][l] + red[3][b][i][l];
-        u[i] = red[0][2 + b][i][l] + red[1][2 + b][i][l] + red[2][2 + b][i][l] + red[3][2 + b][i][l];
+        g[i] = red[0][b][ab][i][l] + red[1][b][ab][i][l] + red[2][b][ab][i][l] + red[3][b][ab][i][l];
+        u[i] = red[0][2 + b][ab][i][l] + red[1][2 + b][ab][i][l] + red[2][2 + b][ab][i][l] + red[3][2 + b][ab][i][l];
     }
     const int64_t col = n0 + 16 * b + 4 * (l >> 4);
     if (MODE == 1) {
@@ -681,13 +595,13 @@ int launch_dma(GemmArgs p, hipStream_t s) {
 
 template <int MODE>
 int launch_gemm(const GemmArgs &p, hipStream_t s) {
-    if (p.m <= kS16MaxM && p.k % (4 * kSStep) == 0) {
-        hipLaunchKernelGGL((gateup_skinny16_kernel<MODE>), dim3((unsigned)(p.n_half / kSN)), dim3(kSThreads), 0, s,
-                           p);
-        CK_RETURN_LAUNCH();
-    }
     if (p.m <= kSMaxM && p.k % (4 * kSStep) == 0) {
-        hipLaunchKernelGGL((gateup_skinny_kernel<MODE>), dim3((unsigned)(p.n_half / kSN)), dim3(kSThreads), 0, s, p);
+        if (p.m <= 16)
+            hipLaunchKernelGGL((gateup_skinny16_kernel<MODE, 1>), dim3((unsigned)(p.n_half / kSN)), dim3(kSThreads),
+                               0, s, p);
+        else
+            hipLaunchKernelGGL((gateup_skinny16_kernel<MODE, 2>), dim3((unsigned)(p.n_half / kSN)), dim3(kSThreads),
+                               0, s, p);
         CK_RETURN_LAUNCH();
     }
     const int64_t grid = (int64_t)p.mtiles * p.ntiles;
