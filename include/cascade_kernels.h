@@ -200,7 +200,8 @@ int ck_cascade_decode(const void *q, const void *prefix_k, const void *prefix_v,
  *   mode 5: d = C[:, :n_half]            mode 7: C only (d not written)
  *   mode 8: C, and d = 0
  * Domain: m >= 1, k >= 64 and k % 16 == 0, n_half % 128 == 0,
- * d_stride >= n_half. silu(x) = x / (1 + exp(-x)).
+ * d_stride >= n_half and d_stride % 4 == 0; a and b 16-byte aligned, d and
+ * workspace 8-byte aligned (CK_E_INVALID_ARG otherwise). silu(x) = x / (1 + exp(-x)).
  * Replaces OPS/f3_floor/op_kernel/kernel_f3_floor.cpp:319-321.
  * ========================================================================== */
 int ck_f3_gateup_epilogue(const void *a, const void *b, void *workspace, void *d, int64_t m,

@@ -82,6 +82,12 @@ def test_gemm_validation():
     assert L.ck_f3_gateup_epilogue(p, p, p, p, 16, 128, 128, 6, 128, None) == -1  # mode 6
     assert L.ck_f3_gateup_epilogue(p, p, None, p, 16, 128, 128, 0, 128, None) == -2  # mode 0 needs C
     assert L.ck_f3_gateup_epilogue(p, p, p, p, 0, 128, 128, 1, 128, None) == -1   # M = 0
+    odd8, odd4 = ctypes.c_void_p(24), ctypes.c_void_p(20)  # 8- but not 16-aligned; 4-aligned
+    assert L.ck_f3_gateup_epilogue(odd8, p, p, p, 16, 128, 128, 1, 128, None) == -1   # a alignment
+    assert L.ck_f3_gateup_epilogue(p, odd8, p, p, 16, 128, 128, 1, 128, None) == -1   # b alignment
+    assert L.ck_f3_gateup_epilogue(p, p, p, odd4, 16, 128, 128, 1, 128, None) == -1   # d alignment
+    assert L.ck_f3_gateup_epilogue(p, p, odd4, p, 16, 128, 128, 0, 128, None) == -1   # C alignment
+    assert L.ck_f3_gateup_epilogue(p, p, p, p, 16, 128, 128, 1, 130, None) == -1   # d_stride % 4
 
 
 def test_cascade_plan_and_validation():

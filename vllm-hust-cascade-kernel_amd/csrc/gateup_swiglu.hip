@@ -635,6 +635,10 @@ extern "C" int ck_f3_gateup_epilogue(const void *a, const void *b, void *workspa
     if (d_stride < n_half || d_stride % 4 != 0) return CK_E_INVALID_ARG;
     if (!a || !b || !d) return CK_E_NULL_PTR;
     if (mode != 1 && !workspace) return CK_E_NULL_PTR;
+    // operand rows are fetched 16 bytes at a time, results stored 8 bytes at a time
+    if (reinterpret_cast<uintptr_t>(a) % 16 != 0 || reinterpret_cast<uintptr_t>(b) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(d) % 8 != 0 || reinterpret_cast<uintptr_t>(workspace) % 8 != 0)
+        return CK_E_INVALID_ARG;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (mode == 3) {
         int64_t blocks = (m * (n_half / 8) + 255) / 256;
