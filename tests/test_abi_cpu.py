@@ -74,6 +74,26 @@ def test_suffix_plan_and_validation():
     assert L.ck_suffix_decode(p, p, p, p, 1, p, 4, 8, 8, 128, 1, 128, 2, 0.1, 128, 1, p, p, p, 1 << 20, None) == -1
 
 
+def test_alignment_rejected_before_launch():
+    """Operand pointers the kernels would read or write 16 bytes at a time must be
+    16-byte aligned; a misaligned one is refused with CK_E_INVALID_ARG (nothing launched)."""
+    L = abi.lib()
+    p, odd = ctypes.c_void_p(16), ctypes.c_void_p(24)
+    # stage-1: misaligned q, then misaligned (padded) lse
+    assert L.ck_fa_fp32_stage1(odd, p, p, p, 1, p, p, None, 1, 1, 1, 1, 8, 8, 128, 1, 128, 0.1, 128, 1, p, p,
+                               None, 0, None) == -1
+    assert L.ck_fa_fp32_stage1(p, p, p, p, 1, p, p, None, 1, 1, 1, 1, 8, 8, 128, 1, 128, 0.1, 128, 1, p, odd,
+                               None, 0, None) == -1
+    # suffix decode: misaligned k
+    assert L.ck_suffix_decode(p, odd, p, p, 1, p, 4, 8, 8, 128, 1, 128, 0, 0.1, 128, 1, p, p, p, 1 << 20,
+                              None) == -1
+    # lse_merge: misaligned o2
+    assert L.ck_lse_merge(p, 0, odd, 0, p, 1, p, 1, p, 0, None, 4, 16, None) == -1
+    # cascade: misaligned suffix v
+    assert L.ck_cascade_decode(p, p, p, p, 1, p, 1, p, odd, p, 1, p, 1, 0, 4, 32, 8, 128, 128, 0.088, 128, 128,
+                               p, p, p, 1 << 30, None) == -1
+
+
 def test_gemm_validation():
     L = abi.lib()
     p = ctypes.c_void_p(16)

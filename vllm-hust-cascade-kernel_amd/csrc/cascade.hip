@@ -94,6 +94,11 @@ extern "C" int ck_cascade_decode(const void *q, const void *prefix_k, const void
     if (!q || !prefix_k || !prefix_v || !prefix_block_table || !prefix_kv_seqlen || !suffix_k || !suffix_v ||
         !suffix_block_table || !suffix_kv_seqlens || !out || !lse_out)
         return CK_E_NULL_PTR;
+    using ck::aligned_to;
+    if (!aligned_to(q, 16) || !aligned_to(prefix_k, 16) || !aligned_to(prefix_v, 16) ||
+        !aligned_to(suffix_k, 16) || !aligned_to(suffix_v, 16) || !aligned_to(out, 8) || !aligned_to(lse_out, 4) ||
+        !aligned_to(workspace, 16))
+        return CK_E_INVALID_ARG;
     if (batch * num_heads > ((int64_t)1 << 31)) return CK_E_INVALID_ARG;
     if (workspace == nullptr || workspace_bytes < L.total) return CK_E_WORKSPACE;
 

@@ -128,6 +128,9 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {
     return (b % kNumXcd) * per + b / kNumXcd;
 }
 
+// Host-side argument check: p is a multiple of n bytes (null counts as aligned).
+inline bool aligned_to(const void *p, uintptr_t n) { return reinterpret_cast<uintptr_t>(p) % n == 0; }
+
 // Raises a kernel's dynamic-LDS limit to `bytes` on the current device, once
 // per device (bit d of `done` records device d). Safe to call from several
 // threads at once: the attribute call is idempotent and the bit is set

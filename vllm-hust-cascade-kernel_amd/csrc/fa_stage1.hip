@@ -563,6 +563,10 @@ int ck::stage1_launch(const void *q, const void *k, const void *v, const int32_t
     if (batch == 0 || num_tokens == 0 || max_q_len == 0) return CK_OK;
     if (!q || !k || !v || !block_table || !kv_seqlens || !out || !lse) return CK_E_NULL_PTR;
     if (q_len_uniform == 0 && (!q_seqlens || !q_start)) return CK_E_NULL_PTR;
+    // q/k/v rows, O rows and the padded LSE (4 copies per store) move 16 bytes per lane
+    if (!aligned_to(q, 16) || !aligned_to(k, 16) || !aligned_to(v, 16) || !aligned_to(out, 16) ||
+        !aligned_to(lse, 16) || !aligned_to(workspace, 16))
+        return CK_E_INVALID_ARG;
     if (num_tokens * num_heads > ((int64_t)1 << 31)) return CK_E_INVALID_ARG;
 
     Plan p;

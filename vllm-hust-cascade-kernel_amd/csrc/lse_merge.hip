@@ -136,6 +136,10 @@ extern "C" int ck_lse_merge(const void *o1, int o1_dtype, const void *o2, int o2
     if (!okdt(o1_dtype) || !okdt(o2_dtype) || !okdt(out_dtype)) return CK_E_INVALID_ARG;
     if (rows == 0) return CK_OK;
     if (!o1 || !o2 || !lse1 || !lse2 || !out) return CK_E_NULL_PTR;
+    // 8 elements per lane per operand: 16 bytes of bf16, 32 of fp32
+    if (!aligned_to(o1, 16) || !aligned_to(o2, 16) || !aligned_to(out, 16) || !aligned_to(lse1, 4) ||
+        !aligned_to(lse2, 4) || !aligned_to(lse_out, 4))
+        return CK_E_INVALID_ARG;
     MergeArgs a{o1, o2, lse1, lse2, out, lse_out, rows, dim, lse1_stride, lse2_stride};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int key = o1_dtype * 4 + o2_dtype * 2 + out_dtype;

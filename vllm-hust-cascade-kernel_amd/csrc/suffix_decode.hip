@@ -881,6 +881,10 @@ extern "C" int ck_suffix_decode(const void *q, const void *k, const void *v, con
     if (bt_cols < 0 || num_blocks < 0 || kv_cap > bt_cols * kPage) return CK_E_INVALID_ARG;
     if (batch == 0) return CK_OK;
     if (!q || !k || !v || !block_table || !kv_seqlens || !out || !lse) return CK_E_NULL_PTR;
+    // q/k/v rows and the workspace partials move up to 16 bytes per lane
+    if (!aligned_to(q, 16) || !aligned_to(k, 16) || !aligned_to(v, 16) || !aligned_to(out, 4) ||
+        !aligned_to(lse, 4) || !aligned_to(workspace, 16))
+        return CK_E_INVALID_ARG;
     const int64_t chunks = num_splits > 0 ? num_splits : suffix_default_chunks(num_heads, kv_heads);
     if (kv_heads * chunks > 0x7FFFFFFF || chunks > (1 << 20)) return CK_E_INVALID_ARG;
     const int64_t per_launch = suffix_group_batch(kv_cap);
