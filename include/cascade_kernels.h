@@ -7,7 +7,11 @@
  * CK_E* code for a rejected argument (nothing is launched), or a positive
  * hipError_t from the launch. Callers own every buffer, including the
  * workspaces whose sizes the *_plan functions report. No entry point
- * allocates or frees device memory.
+ * allocates or frees device memory. Pointers the kernels move 16 bytes at a
+ * time per lane (q, K/V pools, O rows, the padded stage-1 LSE, workspaces)
+ * must be 16-byte aligned, bf16 results written 8 or 4 bytes at a time and
+ * compact LSE arrays 4-byte aligned; a misaligned pointer is refused with
+ * CK_E_INVALID_ARG before any launch.
  *
  * Reference interfaces replaced (paths relative to the reference root,
  * ascend-kernel/csrc/ops/ abbreviated OPS/):
