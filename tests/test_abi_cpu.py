@@ -148,3 +148,6 @@ def test_add_rms_norm_validation_without_launch():
     assert L.ck_add_rms_norm_stats(p, None, p, None, p, p, p, 4, 64, bf16, 0, 1e-6, None) == -2  # x2 in mode 0
     assert L.ck_add_rms_norm_stats(p, p, None, None, p, p, p, 4, 64, bf16, 1, 1e-6, None) == -2  # gamma in mode 1
     assert L.ck_add_rms_norm_stats(None, None, None, None, None, None, None, 0, 64, bf16, 1, 1e-6, None) == 0
+    odd = ctypes.c_void_p(24)
+    assert L.ck_add_rms_norm_stats(odd, p, p, None, p, p, p, 4, 64, bf16, 0, 1e-6, None) == -1  # x1 alignment
+    assert L.ck_add_rms_norm_stats(p, p, odd, None, p, p, p, 4, 64, bf16, 1, 1e-6, None) == -1  # gamma alignment

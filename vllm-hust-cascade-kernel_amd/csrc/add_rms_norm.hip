@@ -222,6 +222,10 @@ extern "C" int ck_add_rms_norm_stats(const void *x1, const void *x2, const void 
     if (mode != 1 && !x2) return CK_E_NULL_PTR;
     if (mode == 0 && !x_out) return CK_E_NULL_PTR;
     if (mode == 1 && (!gamma || !y)) return CK_E_NULL_PTR;
+    // rows, gamma and beta move 16 bytes per lane
+    if (!aligned_to(x1, 16) || !aligned_to(x2, 16) || !aligned_to(gamma, 16) || !aligned_to(beta, 16) ||
+        !aligned_to(x_out, 16) || !aligned_to(y, 16) || !aligned_to(rstd, 4))
+        return CK_E_INVALID_ARG;
     NormArgs a;
     a.x1 = static_cast<const uint16_t *>(x1);
     a.x2 = static_cast<const uint16_t *>(x2);
