@@ -1,25 +1,29 @@
 """Benchmark of the cascade-decode operator set on one MI355X.
 
-Workload (BASELINE config 2 end-to-end, plus config 4 at M=4096):
-  * cascade decode, Llama-3-8B attention shapes: 32 query heads, 8 kv heads,
-    head dim 128, bf16; a shared 8192-token prefix (64 pages of 128 tokens,
-    permuted physical pages) read by stage-1 in the flattened form (one request,
-    q_len = 64); 64 sequences whose own suffixes have geometric lengths (mean 512,
-    clipped to [1, 4096]); the two partial results merged into bf16. The step
-    runs the fused npu.cascade_decode op (stage-1, suffix, merge epilogue); the
-    reference's three-op composition (fa_fp32_stage1, suffix_decode, lse_merge)
-    is timed beside it, and each op alone.
-  * the fused SwiGLU gate_up GEMM, activations [4096, 4096], weight
-    [2*14336, 4096] bf16, fp32 accumulation, d = silu(g) * u in bf16.
-
-value = end-to-end cascade HBM throughput: algorithmic bytes (q, prefix K/V read
-once, every suffix K/V, block tables, seqlens, final bf16 O and merged LSE) /
-measured time of one fused cascade decode. Inputs are resident in HBM; K/V pools rotate through enough copies
+The step (timed exactly --steps times after --warmup untimed steps) is one fused
+npu.cascade_decode call at BASELINE config 2's attention shapes, end to end:
+  32 query heads, 8 kv heads, head dim 128, bf16; a shared 8192-token prefix (64
+  pages of 128 tokens, permuted physical pages) read by stage-1 in the flattened
+  form (one request, q_len = 64); 64 sequences whose own suffixes have geometric
+  lengths (mean 512, clipped to [1, 4096]); the two partial results merged into
+  bf16 O and the merged LSE.
+value = algorithmic bytes of one step (q, prefix K/V read once, every suffix
+K/V, block tables, seqlens, final bf16 O and merged LSE) x steps / the timed
+region. Inputs are resident in HBM; the K/V pools rotate through enough copies
 (>= 2 GiB distinct) that the 256 MB Infinity Cache cannot serve them.
-Each timing loop launches its op back to back on the stream the kernels run on
-(the step loop exactly --steps times, each component op at least 100 times),
-with HIP events only at the loop's two ends (an event recorded between two
-kernels delays the second by several microseconds).
+
+Reported beside it (extra keys, each op launched back to back on the stream its
+kernels run on, HIP events only at a loop's two ends):
+  * each op of the reference's three-op composition, and the composition;
+  * lse_merge of two fp32 partials [8192, 128] (5% of the
+    suffix LSEs -inf) into bf16 + merged LSE, over rotated inputs (HBM) and on
+    one fixed input (labelled cache-hot);
+  * the fused SwiGLU gate_up GEMM at M = 4096 (MFMA-bound) and
+    at M = 1, 16, 256 (weight-stream bound);
+  * the 70B-class cascade (H 64 / KVH 8, 32768-token prefix,
+    256 sequences) followed by the SwiGLU GEMM M = 256, K = 8192, I = 28672;
+  * add_rms_norm_stats, a HIP-graph batch of the cascade, and the CPU baseline
+    (the torch CPU restatement of the same cascade on the host's cores).
 """
 import argparse
 import json
@@ -35,116 +39,128 @@ BF16_PEAK_TFLOPS = 2500.0    # MI355X published dense bf16 MFMA peak
 
 B, H, KVH, D, PREFIX, PAGE = 64, 32, 8, 128, 8192, 128
 GEMM_M, GEMM_K, GEMM_I = 4096, 4096, 14336
+C5 = dict(B=256, H=64, KVH=8, PREFIX=32768, GEMM_M=256, GEMM_K=8192, GEMM_I=28672)
+MERGE_ROWS = 256 * 32        # [B=256, H=32] rows of D = 128
 NORM_M, NORM_K = 2048, 5120  # add_rms_norm_stats at the reference's prefill-main shape
 ROTATE_BYTES = 2 << 30
 # the kernels each op launches (an op's HIP-event time covers all of them)
 OP_KERNELS = {"fa_fp32_stage1": "stage1_kernel + stage1_combine_kernel",
               "suffix_decode": "suffix_stream_kernel + suffix_fixup_kernel",
               "lse_merge": "lse_merge_kernel"}
+CPU_THREADS_MAX = 16         # the GPU box's host-core share for one GPU
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="only the step loop and the cascade's ops")
     return ap.parse_args()
 
 
-def suffix_lengths():
+def geometric_suffixes(n, seed):
     import numpy as np
-    rng = np.random.default_rng(0)
-    return np.clip(rng.geometric(1.0 / 512, size=B), 1, 4096).astype(np.int64)
+    rng = np.random.default_rng(seed)
+    return np.clip(rng.geometric(1.0 / 512, size=n), 1, 4096).astype(np.int64)
 
 
-def build_workload(torch, dev):
+def kv_tok_bytes(kvh):
+    return kvh * D * 2 * 2  # K and V rows of one token, bf16
+
+
+def build_cascade(torch, dev, b, h, kvh, prefix, suf, seed):
+    """Pools rotated over >= ROTATE_BYTES of distinct copies, permuted pages."""
     import numpy as np
-    suf = suffix_lengths()
     nsb = [(int(s) + PAGE - 1) // PAGE for s in suf]
-    npages = PREFIX // PAGE + sum(nsb)
-    rng = np.random.default_rng(1)
+    npages = prefix // PAGE + sum(nsb)
+    rng = np.random.default_rng(seed)
     perm = rng.permutation(npages).astype(np.int32)
-    bt_pre = torch.from_numpy(perm[:PREFIX // PAGE][None, :].copy()).to(dev)
-    bt_suf_np = np.zeros((B, max(nsb)), dtype=np.int32)
-    off = PREFIX // PAGE
-    for b in range(B):
-        bt_suf_np[b, :nsb[b]] = perm[off:off + nsb[b]]
-        off += nsb[b]
+    bt_pre = torch.from_numpy(perm[:prefix // PAGE][None, :].copy()).to(dev)
+    bt_suf_np = np.zeros((b, max(nsb)), dtype=np.int32)
+    off = prefix // PAGE
+    for i in range(b):
+        bt_suf_np[i, :nsb[i]] = perm[off:off + nsb[i]]
+        off += nsb[i]
     bt_suf = torch.from_numpy(bt_suf_np).to(dev)
-    pool_bytes = 2 * npages * PAGE * KVH * D * 2
+    pool_bytes = npages * PAGE * kv_tok_bytes(kvh)
     copies = max(2, -(-ROTATE_BYTES // pool_bytes))
-    g = torch.Generator(device=dev).manual_seed(0)
+    g = torch.Generator(device=dev).manual_seed(seed)
     pools = []
     for _ in range(copies):
-        k = torch.randn(npages, PAGE, KVH, D, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
-        v = torch.randn(npages, PAGE, KVH, D, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
-        q = torch.randn(B, H, D, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        k = torch.randn(npages, PAGE, kvh, D, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        v = torch.randn(npages, PAGE, kvh, D, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        q = torch.randn(b, h, D, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
         pools.append((q, k, v))
-    w = dict(
-        pools=pools, bt_pre=bt_pre, bt_suf=bt_suf,
-        qlens=torch.tensor([B], dtype=torch.int64, device=dev),
-        kvlens=torch.tensor([PREFIX], dtype=torch.int64, device=dev),
-        suf=torch.from_numpy(suf).to(dev), suf_np=suf, npages=npages, copies=copies,
-    )
-    # algorithmic bytes of one cascade step (inputs read once, final output written once)
-    kv_tok = KVH * D * 2 * 2
-    w["bytes_prefix_kernel"] = (B * H * D * 2 + PREFIX * kv_tok + bt_pre.numel() * 4 + 16
-                                + B * H * D * 4 + B * H * 8 * 4)       # stage-1 reads + fp32 O + padded LSE
-    w["bytes_suffix_kernel"] = (B * H * D * 2 + int(suf.sum()) * kv_tok + bt_suf.numel() * 4 + B * 8
-                                + B * H * D * 2 + B * H * 4)            # suffix reads + bf16 O + LSE
-    w["bytes_merge_kernel"] = B * H * D * (4 + 2 + 2) + B * H * (8 + 1) * 4
-    w["bytes_end_to_end"] = (B * H * D * 2 + PREFIX * kv_tok + int(suf.sum()) * kv_tok
-                             + (bt_pre.numel() + bt_suf.numel()) * 4 + (B + 1) * 8 + B * H * D * 2 + B * H * 4)
-    w["flops_prefix"] = 4 * B * H * D * PREFIX
-    return w
+    c = dict(pools=pools, bt_pre=bt_pre, bt_suf=bt_suf, copies=copies, suf_np=suf, B=b, H=h, KVH=kvh,
+             PREFIX=prefix, qlens=torch.tensor([b], dtype=torch.int64, device=dev),
+             kvlens=torch.tensor([prefix], dtype=torch.int64, device=dev), suf=torch.from_numpy(suf).to(dev))
+    kt = kv_tok_bytes(kvh)
+    c["bytes_end_to_end"] = (b * h * D * 2 + prefix * kt + int(suf.sum()) * kt
+                             + (bt_pre.numel() + bt_suf.numel()) * 4 + (b + 1) * 8 + b * h * D * 2 + b * h * 4)
+    c["bytes_stage1"] = (b * h * D * 2 + prefix * kt + bt_pre.numel() * 4 + 16
+                         + b * h * D * 4 + b * h * 8 * 4)            # reads + fp32 O + padded LSE
+    c["bytes_suffix"] = (b * h * D * 2 + int(suf.sum()) * kt + bt_suf.numel() * 4 + b * 8
+                         + b * h * D * 2 + b * h * 4)                # reads + bf16 O + LSE
+    c["bytes_merge"] = b * h * D * (4 + 2 + 2) + b * h * (8 + 1) * 4
+    c["flops_stage1"] = 4 * b * h * D * prefix
+    return c
 
 
 def cpu_baseline(torch):
-    """Times the CPU oracle (numpy restatement, test infrastructure) on full
-    cascade steps of the same workload: einsum loops, one thread (numpy's
-    einsum without optimize= does not call BLAS). One warm-up step, then at
-    least 5 timed steps and at least 10 s of work (at most ~30 s); the median
-    step is reported."""
+    """The torch CPU restatement of the cascade (oracle/torch_cpu.py: 512-column
+    online softmax with bf16 P for stage-1, per-sequence suffix attention, LSE
+    merge) on full steps of the benchmark workload, run with the host's allowed
+    cores (at most the box's 16-core share for one GPU). One warm-up step, then
+    the median of at least 5 steps and at least 10 s of work (at most ~30 s)."""
     import numpy as np
     sys.path.insert(0, REPO)
-    from oracle import attention as A
-    from oracle.merge import merge_fp64
-    suf = suffix_lengths()
-    rng = np.random.default_rng(2)
+    from oracle import torch_cpu as TC
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, CPU_THREADS_MAX))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    suf = geometric_suffixes(B, 0)
     nsb = [(int(s) + PAGE - 1) // PAGE for s in suf]
     npages = PREFIX // PAGE + sum(nsb)
-    k = rng.standard_normal((npages, PAGE, KVH, D)).astype(np.float32)
-    v = rng.standard_normal((npages, PAGE, KVH, D)).astype(np.float32)
-    q = rng.standard_normal((B, H, D)).astype(np.float32)
-    bt_pre = np.arange(PREFIX // PAGE, dtype=np.int32)[None]
-    bt_suf = np.zeros((B, max(nsb)), dtype=np.int32)
+    g = torch.Generator().manual_seed(2)
+    k = torch.randn(npages, PAGE, KVH, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(npages, PAGE, KVH, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+    bt_pre = torch.arange(PREFIX // PAGE, dtype=torch.int32)
+    bt_suf = torch.zeros(B, max(nsb), dtype=torch.int32)
     off = PREFIX // PAGE
     for b in range(B):
-        bt_suf[b, :nsb[b]] = np.arange(off, off + nsb[b])
+        bt_suf[b, :nsb[b]] = torch.arange(off, off + nsb[b], dtype=torch.int32)
         off += nsb[b]
 
     def step():
-        O1, L1 = A.stage1(q, k, v, bt_pre, [B], [PREFIX])
-        O2, L2 = A.suffix(q, k, v, bt_suf, suf)
-        merge_fp64(O1, O2, L1, L2)
+        O1, L1 = TC.stage1(q, k, v, bt_pre, PREFIX)
+        O2, L2 = TC.suffix(q, k, v, bt_suf, suf)
+        out, _ = TC.merge(O1, O2, L1, L2)
+        out.to(torch.bfloat16)
 
     step()  # warm-up
     times = []
     t_start = time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - t_start < 10.0 and len(times) < 64):
+    while len(times) < 5 or (time.perf_counter() - t_start < 10.0 and len(times) < 200):
         t0 = time.perf_counter()
         step()
         times.append(time.perf_counter() - t0)
         if time.perf_counter() - t_start > 30.0:
             break
+    torch.set_num_threads(prev)
     dt = float(np.median(times))
-    kv_tok = KVH * D * 2 * 2
-    nbytes = B * H * D * 2 + PREFIX * kv_tok + int(suf.sum()) * kv_tok + B * H * D * 2
-    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": "full cascade steps of the benchmark workload (stage-1 + suffix + merge) through "
-                      "the numpy oracle: median of %d steps (%.2f s each, %.1f s total) after one warm-up"
-                      % (len(times), dt, sum(times))}
+    kt = kv_tok_bytes(KVH)
+    nbytes = B * H * D * 2 + PREFIX * kt + int(suf.sum()) * kt + B * H * D * 2 + B * H * 4
+    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": "full cascade steps of the benchmark workload (stage-1 + suffix + merge) through the "
+                      "torch CPU restatement (oracle/torch_cpu.py, fp32, %d threads): median of %d steps "
+                      "(%.3f s each, %.1f s total) after one warm-up" % (cores, len(times), dt, sum(times))}
 
 
 def main():
@@ -154,74 +170,17 @@ def main():
               "(the cascade-decode path would shard by kv head, with no exchange between GPUs)" % args.gpus,
               file=sys.stderr)
         sys.exit(2)
+    import numpy as np
     import torch
     import cascade_amd  # noqa: F401
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream()
 
-    w = build_workload(torch, dev)
-    a = torch.randn(GEMM_M, GEMM_K, device=dev, dtype=torch.float32).to(torch.bfloat16)
-    wt = (torch.randn(2 * GEMM_I, GEMM_K, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)
-    d_out = torch.empty(GEMM_M, GEMM_I, device=dev, dtype=torch.bfloat16)
-    ws = torch.empty(GEMM_M, 2 * GEMM_I, device=dev, dtype=torch.bfloat16)
-
-    # calibration copy of known size (read 256 MiB + write 256 MiB) for the PMC
-    # traffic scale factor; outside the timed region
-    src = torch.empty(128 << 20, dtype=torch.int16, device=dev).fill_(1)
-    dst = torch.empty_like(src)
-    dst.copy_(src)
-    torch.cuda.synchronize()
-    del src, dst
-
-    def stage1(i):
-        q, k, v = w["pools"][i % w["copies"]]
-        return torch.ops.npu.fa_fp32_stage1(q, k, v, w["bt_pre"], w["qlens"], w["kvlens"], B)
-
-    def suffix(i):
-        q, k, v = w["pools"][i % w["copies"]]
-        return torch.ops.npu.suffix_decode(q, k, v, w["bt_suf"], w["suf"])
-
-    o1_fix, l1_fix = stage1(0)
-    o2_fix, l2_fix = suffix(0)
-
-    def merge(i):
-        return torch.ops.npu.lse_merge(o1_fix, o2_fix, l1_fix, l2_fix, 1)
-
-    def cascade(i):
-        q, k, v = w["pools"][i % w["copies"]]
-        return torch.ops.npu.cascade_decode(q, k, v, w["bt_pre"], w["kvlens"], k, v, w["bt_suf"], w["suf"])
-
-    def cascade_unfused(i):
-        o1, l1 = stage1(i)
-        o2, l2 = suffix(i)
-        return torch.ops.npu.lse_merge(o1, o2, l1, l2, 1)
-
-    def gemm(i):
-        torch.ops.npu.f3_gateup_epilogue(a, wt, ws, d_out, 1)
-
-    # add_rms_norm_stats inputs, rotated over enough copies to leave the Infinity Cache
-    norm_copies = 8
-    norm_in = [(torch.randn(NORM_M, NORM_K, device=dev) * 0.5).to(torch.bfloat16) for _ in range(2 * norm_copies)]
-    norm_gamma = (1.0 + torch.randn(NORM_K, device=dev) * 0.1).to(torch.bfloat16)
-
-    def norm0(i):
-        j = 2 * (i % norm_copies)
-        return torch.ops.npu.add_rms_norm_stats(norm_in[j], norm_in[j + 1], None, None, 1e-6, 0)
-
-    def norm1(i):
-        j = 2 * (i % norm_copies)
-        return torch.ops.npu.add_rms_norm_stats(norm_in[j], norm_in[j], norm_gamma, None, 1e-6, 1)
-
-    def step(i):
-        cascade(i)
-        gemm(i)
-
-    def timed(fn, n, first, warm=True):
-        """Mean GPU time (ms) of n back-to-back calls, HIP events only at the two
-        ends (an event between kernels costs the stream several microseconds).
-        With `warm`, one untimed call first: a kernel's first launch in the
-        process loads its code object (the step itself has its warmup steps)."""
+    def timed(fn, n, first=0, warm=True):
+        """Mean GPU time (ms) of n back-to-back calls, HIP events on `stream` at
+        the loop's two ends only. With `warm`, one untimed call first (a kernel's
+        first launch in the process loads its code object)."""
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         if warm:
@@ -234,27 +193,139 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n
 
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
+    # ---- the step: fused cascade decode at config 2 shapes ------------------------
+    w = build_cascade(torch, dev, B, H, KVH, PREFIX, geometric_suffixes(B, 0), 1)
 
-    # the timed region: exactly `steps` full steps
+    def cascade(i, c=w):
+        q, k, v = c["pools"][i % c["copies"]]
+        return torch.ops.npu.cascade_decode(q, k, v, c["bt_pre"], c["kvlens"], k, v, c["bt_suf"], c["suf"])
+
+    for i in range(args.warmup):
+        cascade(i)
+    torch.cuda.synchronize()
+    # timed region: synchronize on both sides (one rank: no barrier to take)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ms_step = timed(step, args.steps, args.warmup, warm=False)
+    ms_step = timed(cascade, args.steps, args.warmup, warm=False)
     wall = time.perf_counter() - t0
+    value = w["bytes_end_to_end"] / (ms_step * 1e-3) / 1e9
 
-    # component timings: each op over the same number of back-to-back launches, at
-    # least 100, so the start-up gap between the first event and the first kernel
-    # (a host launch latency) is a small share of the loop
+    # ---- the cascade's ops: the reference's three-op composition -----------------------
+    def stage1(i, c=w):
+        q, k, v = c["pools"][i % c["copies"]]
+        return torch.ops.npu.fa_fp32_stage1(q, k, v, c["bt_pre"], c["qlens"], c["kvlens"], c["B"])
+
+    def suffix(i, c=w):
+        q, k, v = c["pools"][i % c["copies"]]
+        return torch.ops.npu.suffix_decode(q, k, v, c["bt_suf"], c["suf"])
+
+    parts = [(stage1(i), suffix(i)) for i in range(w["copies"])]
+
+    def merge(i):
+        (o1, l1), (o2, l2) = parts[i % len(parts)]
+        return torch.ops.npu.lse_merge(o1, o2, l1, l2, 1)
+
+    def cascade_unfused(i):
+        o1, l1 = stage1(i)
+        o2, l2 = suffix(i)
+        return torch.ops.npu.lse_merge(o1, o2, l1, l2, 1)
+
     n = max(args.steps, 100)
-    ms = {"cascade": timed(cascade, n, 0), "cascade_unfused": timed(cascade_unfused, n, 0), "gemm": timed(gemm, n, 0),
-          "stage1": timed(stage1, n, 0), "suffix": timed(suffix, n, 0), "merge": timed(merge, n, 0),
-          "norm0": timed(norm0, n, 0), "norm1": timed(norm1, n, 0)}
+    ms = {"cascade_unfused": timed(cascade_unfused, n), "stage1": timed(stage1, n), "suffix": timed(suffix, n),
+          "merge": timed(merge, n)}
+    del parts
+    per_op = {"fa_fp32_stage1": (ms["stage1"], w["bytes_stage1"]),
+              "suffix_decode": (ms["suffix"], w["bytes_suffix"]),
+              "lse_merge": (ms["merge"], w["bytes_merge"])}
+    dom = max(per_op, key=lambda k: per_op[k][0])
+    dom_gbs = per_op[dom][1] / (per_op[dom][0] * 1e-3) / 1e9
+    # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    # (calibrated against a plain copy of known size)
+    traffic = {}
+    tpath = os.path.join(REPO, "profiles", "pmc_traffic.json")
+    if os.path.exists(tpath):
+        traffic = json.load(open(tpath))
 
-    # decode-sized SwiGLU GEMMs (BASELINE config 4's other M values) over two weight
-    # copies (470 MB together, beyond the Infinity Cache), so the weight stream is
-    # measured from HBM
+    line = {
+        "metric": "cascade-decode attn HBM GB/s (% of peak) + SwiGLU GEMM TFLOP/s at 1 MI355X",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1) bf16 q/k/v, N(0,0.02) weights, seeded)",
+        "config": {
+            "workload": "BASELINE config 2 end to end: cascade decode H32/KVH8/D128, shared prefix 8192 "
+                        "(flattened stage-1, q_len 64), 64 suffixes ~Geometric(mean 512) clipped [1,4096] "
+                        "(%d tokens), page 128, permuted pages, merge to bf16 + merged LSE; one fused "
+                        "cascade_decode call per step" % int(w["suf_np"].sum()),
+            "kv_rotation_copies": w["copies"],
+            "bytes_per_step": w["bytes_end_to_end"],
+        },
+        "cascade_pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "cascade_us": round(ms_step * 1e3, 2),
+        "cascade_unfused_us": round(ms["cascade_unfused"] * 1e3, 2),
+        "per_op_us": {k: round(v[0] * 1e3, 2) for k, v in per_op.items()},
+        "roofline": {"kernel": dom + " op (" + OP_KERNELS[dom] + ")", "bound": "hbm", "achieved": round(dom_gbs, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic.get(dom)},
+    }
+    if args.no_extras:
+        print(json.dumps(line), flush=True)
+        return
+
+    # ---- the merge alone, fp32 partials into bf16 + merged LSE ------
+    merge_bytes = MERGE_ROWS * D * (4 + 4 + 2) + MERGE_ROWS * 4 * 3
+    m_copies = -(-ROTATE_BYTES // merge_bytes)
+    gm = torch.Generator(device=dev).manual_seed(3)
+    m_in = []
+    for _ in range(m_copies):
+        o1 = torch.randn(MERGE_ROWS, D, generator=gm, device=dev)
+        o2 = torch.randn(MERGE_ROWS, D, generator=gm, device=dev)
+        l1 = torch.randn(MERGE_ROWS, generator=gm, device=dev) * 2.0
+        l2 = torch.randn(MERGE_ROWS, generator=gm, device=dev) * 2.0
+        l2[torch.rand(MERGE_ROWS, generator=gm, device=dev) < 0.05] = -float("inf")
+        m_in.append((o1, o2, l1, l2))
+
+    def merge3(i):
+        return torch.ops.npu.lse_merge_with_lse(*m_in[i % m_copies], 1)
+
+    def merge3_hot(i):
+        return torch.ops.npu.lse_merge_with_lse(*m_in[0], 1)
+    t_m3, t_m3_hot = timed(merge3, n), timed(merge3_hot, n)
+    del m_in
+    line["config3_merge"] = {
+        "rows": MERGE_ROWS, "bytes": merge_bytes, "rotation_copies": m_copies,
+        "us": round(t_m3 * 1e3, 2), "gbs": round(merge_bytes / (t_m3 * 1e-3) / 1e9, 1),
+        "frac_of_hbm_peak": round(merge_bytes / (t_m3 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "cache_hot_us": round(t_m3_hot * 1e3, 2),
+        "cache_hot_gbs": round(merge_bytes / (t_m3_hot * 1e-3) / 1e9, 1)}
+
+    # ---- the fused SwiGLU GEMM ------------------------------------------
+    a = torch.randn(GEMM_M, GEMM_K, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    wt = (torch.randn(2 * GEMM_I, GEMM_K, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+    d_out = torch.empty(GEMM_M, GEMM_I, device=dev, dtype=torch.bfloat16)
+
+    def gemm(i):
+        torch.ops.npu.f3_gateup_epilogue(a, wt, None, d_out, 1)
+    for _ in range(10):  # let the clocks settle under a sustained MFMA load before timing
+        gemm(0)
+    t_gemm = timed(gemm, max(20, n // 5))
+    gemm_tflops = 2.0 * GEMM_M * GEMM_K * 2 * GEMM_I / (t_gemm * 1e-3) / 1e12
+    line["swiglu_gemm"] = {"M": GEMM_M, "K": GEMM_K, "I": GEMM_I, "tflops": round(gemm_tflops, 1),
+                           "us": round(t_gemm * 1e3, 1), "pct_of_bf16_peak": round(100.0 * gemm_tflops /
+                                                                                    BF16_PEAK_TFLOPS, 2)}
+    line["roofline_gemm"] = {"kernel": "f3_gateup_epilogue mode 1", "bound": "mfma", "achieved": round(gemm_tflops, 1),
+                             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(gemm_tflops / BF16_PEAK_TFLOPS, 4),
+                             "traffic": traffic.get("f3_gateup_epilogue")}
+    # decode-sized M over two weight copies (470 MB together, beyond the Infinity Cache)
     wt_pair = [wt, (torch.randn(2 * GEMM_I, GEMM_K, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)]
     small_m = {}
     for mm in (1, 16, 256):
@@ -263,13 +334,69 @@ def main():
 
         def gemm_m(i, a_m=a_m, d_m=d_m):
             torch.ops.npu.f3_gateup_epilogue(a_m, wt_pair[i % 2], None, d_m, 1)
-        t = timed(gemm_m, n, 0)
-        small_m[str(mm)] = {"us": round(t * 1e3, 1),
-                            "weight_gbs": round(2 * GEMM_I * GEMM_K * 2 / (t * 1e-3) / 1e9, 1)}
-    del wt_pair
+        t = timed(gemm_m, n)
+        wbytes = 2 * GEMM_I * GEMM_K * 2
+        small_m[str(mm)] = {"us": round(t * 1e3, 1), "weight_gbs": round(wbytes / (t * 1e-3) / 1e9, 1),
+                            "frac_of_hbm_peak": round((wbytes + mm * (GEMM_K + GEMM_I) * 2) / (t * 1e-3) / 1e9
+                                                      / HBM_PEAK_GBS, 4)}
+    line["swiglu_gemm_small_m"] = small_m
+    del wt_pair, a, wt, d_out
 
-    # HIP-graph batch: one graph holding one fused cascade call per K/V pool copy,
-    # replayed back to back (the plugin's graph mode); launch gaps disappear
+    # ---- 70B-class cascade + SwiGLU GEMM -------------------------
+    c5 = build_cascade(torch, dev, C5["B"], C5["H"], C5["KVH"], C5["PREFIX"], geometric_suffixes(C5["B"], 5), 5)
+    a5 = torch.randn(C5["GEMM_M"], C5["GEMM_K"], device=dev, dtype=torch.float32).to(torch.bfloat16)
+    w5 = (torch.randn(2 * C5["GEMM_I"], C5["GEMM_K"], device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+    d5 = torch.empty(C5["GEMM_M"], C5["GEMM_I"], device=dev, dtype=torch.bfloat16)
+
+    def c5_cascade(i):
+        return cascade(i, c5)
+
+    def c5_gemm(i):
+        torch.ops.npu.f3_gateup_epilogue(a5, w5, None, d5, 1)
+
+    def c5_step(i):
+        c5_cascade(i)
+        c5_gemm(i)
+    t5 = {"cascade": timed(c5_cascade, 30), "gemm": timed(c5_gemm, 30), "step": timed(c5_step, 30)}
+    g5_flops = 2.0 * C5["GEMM_M"] * C5["GEMM_K"] * 2 * C5["GEMM_I"]
+    g5_bytes = 2 * C5["GEMM_I"] * C5["GEMM_K"] * 2 + C5["GEMM_M"] * (C5["GEMM_K"] + C5["GEMM_I"]) * 2
+    line["config5"] = {
+        "workload": "H64/KVH8/D128, shared prefix 32768, 256 suffixes ~Geometric(mean 512) clipped [1,4096] "
+                    "(%d tokens); then SwiGLU GEMM M=256 K=8192 I=28672" % int(c5["suf_np"].sum()),
+        "kv_rotation_copies": c5["copies"],
+        "cascade_us": round(t5["cascade"] * 1e3, 1),
+        "cascade_gbs": round(c5["bytes_end_to_end"] / (t5["cascade"] * 1e-3) / 1e9, 1),
+        "cascade_bytes": c5["bytes_end_to_end"],
+        "stage1_flops": c5["flops_stage1"],
+        "gemm_us": round(t5["gemm"] * 1e3, 1),
+        "gemm_tflops": round(g5_flops / (t5["gemm"] * 1e-3) / 1e12, 1),
+        "gemm_frac_of_hbm_peak": round(g5_bytes / (t5["gemm"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "step_us": round(t5["step"] * 1e3, 1),
+    }
+    del c5, a5, w5, d5
+
+    # ---- add_rms_norm_stats (adjacent op), rotated over 8 input pairs ----------------
+    norm_copies = 8
+    norm_in = [(torch.randn(NORM_M, NORM_K, device=dev) * 0.5).to(torch.bfloat16) for _ in range(2 * norm_copies)]
+    norm_gamma = (1.0 + torch.randn(NORM_K, device=dev) * 0.1).to(torch.bfloat16)
+
+    def norm0(i):
+        j = 2 * (i % norm_copies)
+        return torch.ops.npu.add_rms_norm_stats(norm_in[j], norm_in[j + 1], None, None, 1e-6, 0)
+
+    def norm1(i):
+        j = 2 * (i % norm_copies)
+        return torch.ops.npu.add_rms_norm_stats(norm_in[j], norm_in[j], norm_gamma, None, 1e-6, 1)
+    t_n0, t_n1 = timed(norm0, n), timed(norm1, n)
+    line["add_rms_norm_stats"] = {
+        "shape": [NORM_M, NORM_K], "dtype": "bf16",
+        "mode0_us": round(t_n0 * 1e3, 2),
+        "mode0_gbs": round((3 * NORM_M * NORM_K * 2 + NORM_M * 4) / (t_n0 * 1e-3) / 1e9, 1),
+        "mode1_us": round(t_n1 * 1e3, 2),
+        "mode1_gbs": round((2 * NORM_M * NORM_K * 2 + NORM_K * 2 + NORM_M * 4) / (t_n1 * 1e-3) / 1e9, 1)}
+    del norm_in
+
+    # ---- HIP-graph batch: one graph holding one cascade call per pool copy -----------
     side = torch.cuda.Stream()
     side.wait_stream(stream)
     with torch.cuda.stream(side):
@@ -290,70 +417,11 @@ def main():
         graph.replay()
     e1.record(stream)
     torch.cuda.synchronize()
-    ms["cascade_graph"] = e0.elapsed_time(e1) / (reps * w["copies"])
+    t_graph = e0.elapsed_time(e1) / (reps * w["copies"])
     del graph
+    line["cascade_graph_us"] = round(t_graph * 1e3, 2)
+    line["cascade_graph_gbs"] = round(w["bytes_end_to_end"] / (t_graph * 1e-3) / 1e9, 2)
 
-    cascade_gbs = w["bytes_end_to_end"] / (ms["cascade"] * 1e-3) / 1e9
-    gemm_flops = 2.0 * GEMM_M * GEMM_K * 2 * GEMM_I
-    gemm_tflops = gemm_flops / (ms["gemm"] * 1e-3) / 1e12
-    per_kernel = {
-        "fa_fp32_stage1": (ms["stage1"], w["bytes_prefix_kernel"]),
-        "suffix_decode": (ms["suffix"], w["bytes_suffix_kernel"]),
-        "lse_merge": (ms["merge"], w["bytes_merge_kernel"]),
-    }
-    dom = max(per_kernel, key=lambda n: per_kernel[n][0])
-    dom_gbs = per_kernel[dom][1] / (per_kernel[dom][0] * 1e-3) / 1e9
-    # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
-    # (calibrated against a plain copy of known size)
-    traffic = gemm_traffic = None
-    tpath = os.path.join(REPO, "profiles", "pmc_traffic.json")
-    if os.path.exists(tpath):
-        tj = json.load(open(tpath))
-        traffic = tj.get(dom)
-        gemm_traffic = tj.get("f3_gateup_epilogue")
-
-    line = {
-        "metric": "cascade-decode attn HBM GB/s (% of peak) + SwiGLU GEMM TFLOP/s at 1 MI355X",
-        "value": round(cascade_gbs, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4),
-        "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (N(0,1) bf16 q/k/v, N(0,0.02) weights, seeded)",
-        "config": {
-            "workload": "cascade decode H32/KVH8/D128, shared prefix 8192 (flattened stage-1, q_len 64), "
-                        "64 suffixes ~Geometric(mean 512) clipped [1,4096] (%d tokens), page 128, permuted "
-                        "pages, merge to bf16; plus fused SwiGLU gate_up GEMM M=%d K=%d I=%d"
-                        % (int(w["suf_np"].sum()), GEMM_M, GEMM_K, GEMM_I),
-            "kv_rotation_copies": w["copies"],
-        },
-        "cascade_pct_of_hbm_peak": round(100.0 * cascade_gbs / HBM_PEAK_GBS, 2),
-        "cascade_us": round(ms["cascade"] * 1e3, 2),
-        "cascade_unfused_us": round(ms["cascade_unfused"] * 1e3, 2),
-        "cascade_graph_us": round(ms["cascade_graph"] * 1e3, 2),
-        "cascade_graph_gbs": round(w["bytes_end_to_end"] / (ms["cascade_graph"] * 1e-3) / 1e9, 2),
-        "per_op_us": {n: round(v[0] * 1e3, 2) for n, v in per_kernel.items()},
-        "add_rms_norm_stats": {
-            "shape": [NORM_M, NORM_K], "dtype": "bf16",
-            "mode0_us": round(ms["norm0"] * 1e3, 2),
-            "mode0_gbs": round((3 * NORM_M * NORM_K * 2 + NORM_M * 4) / (ms["norm0"] * 1e-3) / 1e9, 1),
-            "mode1_us": round(ms["norm1"] * 1e3, 2),
-            "mode1_gbs": round((2 * NORM_M * NORM_K * 2 + NORM_K * 2 + NORM_M * 4) / (ms["norm1"] * 1e-3) / 1e9, 1)},
-        "swiglu_gemm": {"tflops": round(gemm_tflops, 1), "us": round(ms["gemm"] * 1e3, 1),
-                        "pct_of_bf16_peak": round(100.0 * gemm_tflops / BF16_PEAK_TFLOPS, 2)},
-        "swiglu_gemm_small_m": small_m,
-        "roofline": {"kernel": dom + " op (" + OP_KERNELS[dom] + ")", "bound": "hbm", "achieved": round(dom_gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
-        "roofline_gemm": {"kernel": "f3_gateup_epilogue mode 1", "bound": "mfma", "achieved": round(gemm_tflops, 1),
-                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                          "frac": round(gemm_tflops / BF16_PEAK_TFLOPS, 4), "traffic": gemm_traffic},
-    }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(line), flush=True)

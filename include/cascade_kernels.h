@@ -9,9 +9,10 @@
  * workspaces whose sizes the *_plan functions report. No entry point
  * allocates or frees device memory. Pointers the kernels move 16 bytes at a
  * time per lane (q, K/V pools, O rows, the padded stage-1 LSE, workspaces)
- * must be 16-byte aligned, bf16 results written 8 or 4 bytes at a time and
- * compact LSE arrays 4-byte aligned; a misaligned pointer is refused with
- * CK_E_INVALID_ARG before any launch.
+ * must be 16-byte aligned, bf16 results and the GEMM workspace (written or
+ * read 8 bytes at a time) 8-byte aligned and compact LSE arrays 4-byte
+ * aligned; a misaligned pointer is refused with CK_E_INVALID_ARG before any
+ * launch.
  *
  * Reference interfaces replaced (paths relative to the reference root,
  * ascend-kernel/csrc/ops/ abbreviated OPS/):
@@ -139,9 +140,12 @@ int ck_fa_fp32_stage1(const void *q, const void *k, const void *v, const int32_t
  *   lse          fp32 [batch * num_heads] (compact); a sequence with kv length 0
  *                gets out = 0 and lse = -inf (an empty suffix)
  *   kv_cap       upper bound of kv_seqlens(b), <= bt_cols * 128
- *   num_splits   workgroups per kv head that share the list of 64-token windows
- *                (<= 0: the plan's count, as many as are resident at once);
- *                the plan sizes the workspace for it
+ *   num_splits   workgroups per kv head group that share the list of 64-token
+ *                windows (<= 0: the plan's count, as many as are resident at
+ *                once); the plan sizes the workspace for it. A GQA group of
+ *                more than 8 query heads per kv head is split into the fewest
+ *                equal groups of at most 8, each streamed as its own kv head
+ *                group (the K/V pages are then read once per group).
  * Same softmax arithmetic as ck_fa_fp32_stage1 (fp32 accumulation).
  * Replaces the closed CANN op npu_fused_infer_attention_score_v2 used as
  * stage 2 (ascend-kernel/README.md:186-197).

@@ -13,6 +13,11 @@ reference's fp64 semantic model of the stage-1 kernel) without ml_dtypes:
                         h // (H / KVH) (fa_fp32_ref.py:102).
 * ``stage1_tieband`` -- fa_fp32_ref.py:150-206: the same plus the per-element bound
                         A of bf16 near-tie rounding flips (kernel gate |O - O_ref| <= A + floor).
+                        One deliberate difference: a chunk's ambiguity is decayed by every
+                        later running-max step (amb = dm*amb + X, as acc is), where
+                        fa_fp32_ref.py:200-201 scales it by its own step only
+                        (amb += dm*X), which is not a bound once the max moves. Pinned by
+                        brute force over all rounding flips (test_oracle_attention.py).
 * ``stage1_rowwise`` -- fa_fp32_ref.py:209-245: scalar per-row loop (cross-check).
 * ``pack_lse``       -- the padded LSE layout: row (t*H + h) of 8 identical fp32
                         (.../block_epilogue_rescale_o_no_split_row.hpp:409-416,
@@ -52,51 +57,65 @@ def stage1(q, k, v, block_table, q_seqlens, kv_seqlens, chunk=CHUNK, quantize_p=
     q [T,H,D], k/v [numBlocks,128,KVH,D] (any float dtype holding the bf16 values),
     block_table [B,cols] int, q_seqlens/kv_seqlens [B].
     Returns (O [T,H,D] fp64, LSE [T,H] fp64) and, with ``tieband``, A [T,H,D].
+
+    Query head h reads kv head h // (H / KVH) (fa_fp32_ref.py:102); the products
+    run per kv head over its group of query heads (batched BLAS), and requests
+    that read the same pages with the same kv length are computed together.
+    Every query row is independent, so neither changes the arithmetic.
     """
     q64 = np.asarray(q, dtype=np.float64)
-    k64 = np.asarray(k, dtype=np.float64)
-    v64 = np.asarray(v, dtype=np.float64)
     T, H, D = q64.shape
-    KVH = k64.shape[2]
+    KVH = k.shape[2]
     group = H // KVH
     if scale is None:
         scale = float(np.float32(1.0 / np.sqrt(float(D))))
-    heads = np.arange(H) // group
     O = np.zeros((T, H, D))
     LSE = np.full((T, H), -np.inf)
     A = np.zeros((T, H, D)) if tieband else None
     offs = _q_offsets(q_seqlens)
+    work = {}
     for b in range(len(q_seqlens)):
         kv = int(kv_seqlens[b])
         t0, t1 = int(offs[b]), int(offs[b + 1])
         if t1 == t0 or kv <= 0:
             continue
-        kb, vb = gather_kv(k64, v64, block_table[b], kv)
-        kh = kb[:, heads, :]                      # [kv, H, D]
-        vh = vb[:, heads, :]
-        qb = q64[t0:t1].transpose(1, 0, 2)        # [H, Tb, D]
-        m = np.full((H, t1 - t0), -np.inf)
-        gl = np.zeros((H, t1 - t0))
-        acc = np.zeros((H, t1 - t0, D))
-        amb = np.zeros((H, t1 - t0, D)) if tieband else None
+        nblk = (kv + BLOCK_SIZE - 1) // BLOCK_SIZE
+        pages = np.asarray(block_table[b][:nblk], dtype=np.int64)
+        key = (kv, pages.tobytes())
+        work.setdefault(key, (pages, []))[1].append(np.arange(t0, t1))
+    for (kv, _), (pages, toks) in work.items():
+        rows = np.concatenate(toks)
+        Tg = len(rows)
+        kb, vb = gather_kv(k, v, pages, kv)
+        kb = np.asarray(kb, dtype=np.float64).transpose(1, 2, 0)   # [KVH, D, kv]
+        vb = np.asarray(vb, dtype=np.float64).transpose(1, 0, 2)   # [KVH, kv, D]
+        # [KVH, group * Tg, D]: row (a, t) is query head g * group + a of token rows[t]
+        qb = q64[rows].reshape(Tg, KVH, group, D).transpose(1, 2, 0, 3).reshape(KVH, group * Tg, D)
+        m = np.full((KVH, group * Tg), -np.inf)
+        gl = np.zeros((KVH, group * Tg))
+        acc = np.zeros((KVH, group * Tg, D))
+        amb = np.zeros((KVH, group * Tg, D)) if tieband else None
         step = kv if chunk is None else chunk
         for s in range(0, kv, step):
             e = min(kv, s + step)
-            sc = np.einsum('htd,khd->htk', qb, kh[s:e]) * scale
+            sc = np.matmul(qb, kb[:, :, s:e]) * scale
             m_new = np.maximum(m, sc.max(axis=2))
             dm = np.exp(m - m_new) if s > 0 else np.ones_like(m_new)
             ls = np.exp(sc - m_new[:, :, None])
             p = round_bf16(ls).astype(np.float64) if quantize_p else ls
             gl = dm * gl + ls.sum(axis=2)
-            acc = dm[:, :, None] * acc + np.einsum('htk,khd->htd', p, vh[s:e])
+            acc = dm[:, :, None] * acc + np.matmul(p, vb[:, s:e])
             if tieband:
-                amb = dm[:, :, None] * amb + np.einsum(
-                    'htk,khd->htd', _tie_ambiguity(ls, tie_band_rel), np.abs(vh[s:e]))
+                amb = dm[:, :, None] * amb + np.matmul(_tie_ambiguity(ls, tie_band_rel), np.abs(vb[:, s:e]))
             m = m_new
-        O[t0:t1] = (acc / gl[:, :, None]).transpose(1, 0, 2)
-        LSE[t0:t1] = (np.log(gl) + m).T
+
+        def unfold(x):  # [KVH, group * Tg, ...] -> [Tg, H, ...]
+            x = x.reshape(KVH, group, Tg, *x.shape[2:])
+            return np.moveaxis(x, 2, 0).reshape(Tg, H, *x.shape[3:])
+        O[rows] = unfold(acc / gl[:, :, None])
+        LSE[rows] = unfold(np.log(gl) + m)
         if tieband:
-            A[t0:t1] = (amb / gl[:, :, None]).transpose(1, 0, 2)
+            A[rows] = unfold(amb / gl[:, :, None])
     if tieband:
         return O, LSE, A
     return O, LSE

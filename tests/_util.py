@@ -5,6 +5,15 @@ import numpy as np
 
 BF16_EPS = 2.0 ** -8
 
+# (case, max |O error|, O bound, max LSE relative error, LSE bound) of every parity
+# case that records its margin; conftest prints the table after the run.
+MARGINS = []
+
+
+def record_margin(case, o_err, o_bound, l_rel=None, l_bound=None):
+    MARGINS.append((case, float(o_err), float(o_bound), None if l_rel is None else float(l_rel),
+                    None if l_bound is None else float(l_bound)))
+
 
 def torch_bf16(bits, device):
     """uint16 bfloat16 bit patterns (numpy) -> torch.bfloat16 tensor on device."""

@@ -24,6 +24,19 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
 
 
+def pytest_terminal_summary(terminalreporter):
+    """Per-case error margins of the parity tests that record them: the measured
+    max error next to the tolerance it is held to."""
+    from tests._util import MARGINS
+    if not MARGINS:
+        return
+    tr = terminalreporter
+    tr.write_sep("-", "parity margins (max error / bound)")
+    for case, oe, ob, le, lb in MARGINS:
+        lse = "" if le is None else "  LSE rel %.2e / %.0e" % (le, lb)
+        tr.write_line("%-48s O %.3e / %.0e (%5.1f%%)%s" % (case, oe, ob, 100.0 * oe / ob, lse))
+
+
 @pytest.fixture(scope="session")
 def golden_dir():
     return GOLDEN

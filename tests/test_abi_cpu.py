@@ -68,7 +68,11 @@ def test_suffix_plan_and_validation():
     assert abi.suffix_plan(64, 8, 1, 128, 4096)[0] == 256
     L = abi.lib()
     out = ctypes.c_int64(0)
-    assert L.ck_suffix_decode_plan(4, 64, 4, 128, 100, ctypes.byref(out), ctypes.byref(out)) == -4  # group 16
+    # 16 query heads per kv head: two kv head groups of 8, one workgroup per CU
+    assert abi.suffix_plan(4, 64, 4, 128, 128)[0] == 256 // 8
+    # 12 per kv head: two groups of 6; 11 (prime): eleven groups of 1, two workgroups per CU
+    assert abi.suffix_plan(4, 48, 4, 128, 128)[0] == 256 // 8
+    assert abi.suffix_plan(4, 11, 1, 128, 128)[0] == 2 * 256 // 11
     p = ctypes.c_void_p(16)
     assert L.ck_suffix_decode(p, p, p, p, 1, p, 0, 8, 8, 128, 1, 128, 0, 0.1, 128, 1, p, p, None, 0, None) == 0
     assert L.ck_suffix_decode(p, p, p, p, 1, p, 4, 8, 8, 128, 1, 128, 2, 0.1, 128, 1, p, p, p, 1 << 20, None) == -1
@@ -84,9 +88,11 @@ def test_alignment_rejected_before_launch():
                                None, 0, None) == -1
     assert L.ck_fa_fp32_stage1(p, p, p, p, 1, p, p, None, 1, 1, 1, 1, 8, 8, 128, 1, 128, 0.1, 128, 1, p, odd,
                                None, 0, None) == -1
-    # suffix decode: misaligned k
+    # suffix decode: misaligned k; bf16 out 4- but not 8-aligned (the fix-up stores 8 bytes)
     assert L.ck_suffix_decode(p, odd, p, p, 1, p, 4, 8, 8, 128, 1, 128, 0, 0.1, 128, 1, p, p, p, 1 << 20,
                               None) == -1
+    assert L.ck_suffix_decode(p, p, p, p, 1, p, 4, 8, 8, 128, 1, 128, 0, 0.1, 128, 1, ctypes.c_void_p(20), p, p,
+                              1 << 20, None) == -1
     # lse_merge: misaligned o2
     assert L.ck_lse_merge(p, 0, odd, 0, p, 1, p, 1, p, 0, None, 4, 16, None) == -1
     # cascade: misaligned suffix v
@@ -117,7 +123,8 @@ def test_cascade_plan_and_validation():
     assert abi.cascade_plan(0, 32, 8, 128, 8192, 4096) == 0
     L = abi.lib()
     out = ctypes.c_int64(0)
-    assert L.ck_cascade_decode_plan(4, 64, 4, 128, 128, 128, ctypes.byref(out)) == -4   # 16 heads per kv head
+    assert L.ck_cascade_decode_plan(4, 64, 4, 128, 128, 128, ctypes.byref(out)) == 0    # 16 heads per kv head
+    assert L.ck_cascade_decode_plan(4, 11, 1, 128, 128, 128, ctypes.byref(out)) == 0    # 11 heads per kv head
     assert L.ck_cascade_decode_plan(4, 32, 8, 64, 128, 128, ctypes.byref(out)) == -4    # D != 128
     assert L.ck_cascade_decode_plan(4, 30, 8, 128, 128, 128, ctypes.byref(out)) == -1   # H % KVH
     assert L.ck_cascade_decode_plan(4, 32, 8, 128, 128, 128, None) == -2

@@ -57,3 +57,47 @@ def test_full_block_table():
     assert bt.tolist() == [[7, 3, 9, 1, 2], [7, 3, 9, 5, 6], [7, 3, 9, 8, 0]]
     with pytest.raises(ValueError):
         G.full_decode(None, None, None, pre, 100, suf, None)
+
+
+def _meta_case(B=4, H=32, KVH=8, P=1000):
+    import cascade_amd  # noqa: F401  (registers the ops; Meta kernels need no GPU)
+    m = "meta"
+    bf = dict(dtype=torch.bfloat16, device=m)
+    q = torch.empty(B, H, 128, **bf)
+    kv = torch.empty(40, 128, KVH, 128, **bf)
+    btp = torch.empty(1, 8, dtype=torch.int32, device=m)
+    bts = torch.empty(B, 4, dtype=torch.int32, device=m)
+    sl = torch.empty(B, dtype=torch.int64, device=m)
+    return q, kv, btp, bts, sl
+
+
+def test_unaligned_prefix_takes_cascade_without_measuring():
+    g = G.CascadeGate(32, 8, timer=lambda *a: pytest.fail("an unaligned prefix must not be measured"))
+    q, kv, btp, bts, sl = _meta_case()
+    out, lse = g.decode(q, kv, kv, btp, 1000, bts, sl)
+    assert out.shape == q.shape and lse.shape == (4 * 32,)
+    assert not g.decisions
+
+
+def test_capture_needs_decisions_and_prefix_tensors(monkeypatch):
+    """Under capture an unmeasured bucket and an unseen prefix length are refused
+    with a clear error; measured decisions and a cached (or passed) prefix tensor
+    dispatch without a host round trip."""
+    q, kv, btp, bts, sl = _meta_case()
+    g = G.CascadeGate(32, 8, timer=lambda form, b, s: 1.0 if form == G.CASCADE else 2.0)
+    monkeypatch.setattr(G, "_capturing", lambda: True)
+    with pytest.raises(RuntimeError, match="no decision"):
+        g.decode(q, kv, kv, btp, 1024, bts, sl)
+    monkeypatch.setattr(G, "_capturing", lambda: False)
+    g.choose(4, 1024)
+    monkeypatch.setattr(G, "_capturing", lambda: True)
+    with pytest.raises(RuntimeError, match="prefix length 1024"):
+        g.decode(q, kv, kv, btp, 1024, bts, sl)
+    out, _ = g.decode(q, kv, kv, btp, 1024, bts, sl, prefix_len_tensor=torch.empty(1, dtype=torch.int64,
+                                                                                    device="meta"))
+    assert out.shape == q.shape
+    monkeypatch.setattr(G, "_capturing", lambda: False)
+    g.decode(q, kv, kv, btp, 1024, bts, sl)              # eager call makes the tensor once
+    monkeypatch.setattr(G, "_capturing", lambda: True)
+    out, _ = g.decode(q, kv, kv, btp, 1024, bts, sl)     # now capture-safe
+    assert out.shape == q.shape

@@ -93,6 +93,51 @@ def test_full_width_tile_two_m_tiles(mode):
         assert np.array_equal(bf16_to_np(d)[rows], c[:, :I])
 
 
+@pytest.mark.parametrize("mode", [1, 0])
+@pytest.mark.parametrize("M", [1, 17, 300])
+@pytest.mark.parametrize("K", [80, 144, 4112])
+def test_register_staged_kernel_k_not_multiple_of_32(K, M, mode):
+    """K % 16 == 0 but K % 32 != 0 (inside the reference's domain, f3_floor.cpp:64-80)
+    takes the register-staged kernel (the DMA ring steps K by 32 and the decode-sized
+    kernel needs K % 256 == 0): SwiGLU (mode 1) and the gate window with C (mode 0)."""
+    I = 256 if M < 300 else 128
+    a16, b16 = _inputs(M, K, I, seed=500 + K + M + mode)
+    a, b = bits_to_f32(a16), bits_to_f32(b16)
+    d, ws = torch.ops.npu.f3_gateup_epilogue(torch_bf16(a16, DEV), torch_bf16(b16, DEV), None, None, mode)
+    if mode == 1:
+        _swiglu_check(bf16_to_np(d), a, b)
+    else:
+        c = bf16_to_np(ws)
+        _c_check(c, a, b)
+        assert np.array_equal(bf16_to_np(d), c[:, :I])
+
+
+def test_swiglu_config5_shape_sampled_rows():
+    """BASELINE config 5's GEMM leg: M = 256, K = 8192, weight [2 * 28672, 8192] ~
+    N(0, 0.02) (generated on the device from a seeded torch generator). Sampled rows
+    are checked against the fp64 SwiGLU; the fp64 products run over column blocks of
+    the weight so the host never holds it in fp64."""
+    M, K, I = 256, 8192, 28672
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(55)
+    w = (torch.randn(2 * I, K, generator=gen, device=DEV) * 0.02).to(torch.bfloat16)
+    a16 = bf16_bits(np.random.default_rng(56).standard_normal((M, K)))
+    d, _ = torch.ops.npu.f3_gateup_epilogue(torch_bf16(a16, DEV), w, None, None, 1)
+    rows = np.concatenate([np.random.default_rng(57).choice(M, 14, replace=False), [0, M - 1]])
+    a = bits_to_f32(a16)[rows].astype(np.float64)
+    wc = w.cpu()
+    dn = bf16_to_np(d)[rows]
+    exact = np.empty((len(rows), I))
+    step = 4096
+    for j in range(0, I, step):
+        g = bf16_to_np(wc[j:j + step]).astype(np.float64)
+        u = bf16_to_np(wc[I + j:I + j + step]).astype(np.float64)
+        exact[:, j:j + step] = G.silu(a @ g.T) * (a @ u.T)
+    rms = np.sqrt(np.mean(exact ** 2))
+    err = np.abs(dn - exact)
+    assert np.all(err <= 1e-2 * np.abs(exact) + 1e-2 * rms), (err.max(), rms)
+
+
 @pytest.mark.parametrize("M", [1, 16, 256])
 def test_swiglu_config4_shapes(M):
     """K=4096, weight [2*14336, 4096] ~ N(0, 0.02)."""
@@ -214,6 +259,26 @@ def test_mode3_epilogue_only_and_inplace_d():
     d_in = ws2[:, :I]
     d0, _ = torch.ops.npu.f3_gateup_epilogue(a, b, ws2, d_in, 0)
     assert d0.stride(0) == 2 * I and torch.equal(ws2[:, :I], ws[:, :I]) and torch.equal(ws2[:, I:], ws[:, I:])
+
+
+def test_mode3_workspace_eight_byte_aligned():
+    """Mode 3 reads the workspace 8 bytes at a time, so a workspace that is 8- but
+    not 16-byte aligned (the ABI's contract) copies the same gate window."""
+    M, K, I = 20, 128, 256
+    a16, b16 = _inputs(M, K, I, seed=13)
+    a, b = torch_bf16(a16, DEV), torch_bf16(b16, DEV)
+    _, ws = torch.ops.npu.f3_gateup_epilogue(a, b, None, None, 2)
+    buf = torch.zeros(M * 2 * I + 8, dtype=torch.bfloat16, device=DEV)
+    off = next(o for o in range(0, 8, 4) if (buf.data_ptr() + 2 * o) % 16 == 8)
+    ws8 = buf[off:off + M * 2 * I].view(M, 2 * I)
+    ws8.copy_(ws)
+    assert ws8.data_ptr() % 16 == 8
+    d = torch.empty(M, I, dtype=torch.bfloat16, device=DEV)
+    from cascade_amd import abi
+    abi.check(abi.lib().ck_f3_gateup_epilogue(a.data_ptr(), b.data_ptr(), ws8.data_ptr(), d.data_ptr(), M, I, K, 3,
+                                              I, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert torch.equal(d, ws[:, :I])
 
 
 def test_mode1_matches_window_swiglu_of_c():

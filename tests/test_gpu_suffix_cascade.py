@@ -59,6 +59,10 @@ SUFFIX_CASES = [
     ("gqa8_h64", 5, [700, 90, 1025, 2, 4000], 64, 8),
     ("mha_h8_kvh8", 4, [100, 200, 300, 400], 8, 8),
     ("group2", 4, [257, 33, 1000, 5], 8, 4),
+    # more than 8 query heads per kv head: split into groups of <= 8 that share the kv head
+    ("gqa16_h64_kvh4", 5, [700, 0, 1025, 64, 3000], 64, 4),
+    ("gqa12_h48_kvh4", 3, [129, 2000, 1], 48, 4),
+    ("gqa11_h11_kvh1", 3, [500, 77, 1300], 11, 1),
 ]
 
 
@@ -127,8 +131,15 @@ CASCADE_CFGS = [
     (6, 64, 8, 640, "long_cut"),     # G = 8; suffixes cut across workgroups
     (40, 16, 2, 0, "no_prefix"),     # empty prefix: the suffix alone
     (3, 8, 8, 256, "all_empty"),     # every suffix empty: the prefix alone
+    (6, 64, 4, 640, "long_cut"),     # 16 query heads per kv head: two kv head groups
 ]
-CASCADE_IDS = ["config1_b8_h8", "b16_h32_geo", "empty_suffix", "gqa8_long_cut", "empty_prefix", "all_suffix_empty"]
+CASCADE_IDS = ["config1_b8_h8", "b16_h32_geo", "empty_suffix", "gqa8_long_cut", "empty_prefix", "all_suffix_empty",
+               "gqa16_long_cut"]
+# the three-op composition cannot take an empty prefix: fa_fp32_stage1 requires kv
+# seqlens >= 1 (the reference's op_host contract), so that case runs fused only
+CASCADE_RUNS = [(cfg, fused) for cfg in CASCADE_CFGS for fused in (True, False) if fused or cfg[3] > 0]
+CASCADE_RUN_IDS = ["%s-%s" % (CASCADE_IDS[CASCADE_CFGS.index(c)], "fused" if f else "unfused")
+                   for c, f in CASCADE_RUNS]
 
 
 def _cascade_case(cfg):
@@ -162,15 +173,12 @@ def _cascade_run(fused, B, P, q, k, v, bt_pre, bt_suf, suf):
     return bf16_to_np(out), (None if lse is None else lse.cpu().numpy())
 
 
-@pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
-@pytest.mark.parametrize("cfg", CASCADE_CFGS, ids=CASCADE_IDS)
+@pytest.mark.parametrize("cfg,fused", CASCADE_RUNS, ids=CASCADE_RUN_IDS)
 def test_cascade_equals_dense_over_concat(cfg, fused):
     """Config 1 shape (and more): cascade decode == softmax attention over the
     concatenated prefix + suffix KV (bf16 output), for the fused op and for the
     reference's three-op composition; the fused op's merged LSE matches too."""
     B, H, KVH, P, q16, k16, v16, bt_pre, bt_suf, suf = _cascade_case(cfg)
-    if not fused and P == 0:
-        pytest.skip("fa_fp32_stage1 requires kv seqlens >= 1 (reference op_host contract)")
     q, k, v = (torch_bf16(x, DEV) for x in (q16, k16, v16))
     got, lse = _cascade_run(fused, B, P, q, k, v, bt_pre, bt_suf, suf)
     qf, kf, vf = bits_to_f32(q16), bits_to_f32(k16), bits_to_f32(v16)
@@ -348,3 +356,32 @@ def test_cascade_bnsd_suffix_pool_matches_nhd():
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
     with pytest.raises(RuntimeError, match="cascade_decode"):
         cascade_amd.ops.cascade_decode(q, k, v, btp, plen, k, v, bts, sl, 2)
+
+
+@pytest.mark.parametrize("case", [SUFFIX_CASES[1], SUFFIX_CASES[3]], ids=[SUFFIX_CASES[1][0], SUFFIX_CASES[3][0]])
+def test_suffix_bnsd_layout_against_oracle(case):
+    """A BNSD pool [blocks, KVH, 128, 128] built directly (not copied from an NHD
+    pool), called through the C ABI with kv_layout = CK_KV_BNSD and checked against
+    the oracle on the same logical K/V."""
+    from cascade_amd import abi
+    name, B, kvs, H, KVH = case
+    inp = paged_inputs(B, kvs, H, KVH, seed=len(name) + 21, permute=True)
+    k_bnsd = np.ascontiguousarray(inp["k16"].transpose(0, 2, 1, 3))
+    v_bnsd = np.ascontiguousarray(inp["v16"].transpose(0, 2, 1, 3))
+    q = torch_bf16(inp["q16"], DEV)
+    k = torch_bf16(k_bnsd, DEV)
+    v = torch_bf16(v_bnsd, DEV)
+    bt = torch.from_numpy(inp["block_table"]).to(DEV)
+    kl = torch.from_numpy(inp["kv_seqlens"]).to(DEV)
+    cap = bt.shape[1] * 128
+    s, wsb = abi.suffix_plan(B, H, KVH, 128, cap)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    out = torch.empty(B, H, 128, dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty(B * H, dtype=torch.float32, device=DEV)
+    rc = abi.lib().ck_suffix_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), bt.shape[1],
+                                    kl.data_ptr(), B, H, KVH, 128, k.shape[0], 128, abi.CK_KV_BNSD,
+                                    float(np.float32(1 / np.sqrt(128))), cap, s, out.data_ptr(), lse.data_ptr(),
+                                    ws.data_ptr(), wsb, torch.cuda.current_stream().cuda_stream)
+    abi.check(rc)
+    torch.cuda.synchronize()
+    _check_suffix(inp, bf16_to_np(out), lse.cpu().numpy(), H)

@@ -85,8 +85,9 @@ def test_suffix_shapes_and_rejections():
     kl = torch.empty(16, dtype=torch.int64, device=M)
     out, lse = torch.ops.npu.suffix_decode(q, kv, kv, bt, kl)
     assert out.shape == (16, 32, 128) and out.dtype == torch.bfloat16 and lse.shape == (16 * 32,)
-    with pytest.raises(RuntimeError, match="at most 8 query heads"):
-        torch.ops.npu.suffix_decode(_bf(16, 64, 128), _bf(20, 128, 2, 128), _bf(20, 128, 2, 128), bt, kl)
+    # 32 query heads per kv head (kv head groups of 8) are accepted
+    out, _ = torch.ops.npu.suffix_decode(_bf(16, 64, 128), _bf(20, 128, 2, 128), _bf(20, 128, 2, 128), bt, kl)
+    assert out.shape == (16, 64, 128)
     with pytest.raises(RuntimeError, match="batch entries"):
         torch.ops.npu.suffix_decode(q, kv, kv, bt[:3], kl)
 
@@ -124,8 +125,8 @@ def test_cascade_shapes_and_rejections():
         torch.ops.npu.cascade_decode(q, kv, kv, btp, torch.empty(2, dtype=torch.int64, device=M), kv, kv, bts, sl)
     with pytest.raises(RuntimeError, match="cascade_decode: suffix block_table rows"):
         torch.ops.npu.cascade_decode(q, kv, kv, btp, plen, kv, kv, bts[:3], sl)
-    with pytest.raises(RuntimeError, match="cascade_decode: at most 8 query heads"):
-        kv2 = _bf(20, 128, 2, 128)
-        torch.ops.npu.cascade_decode(_bf(16, 64, 128), kv2, kv2, btp, plen, kv2, kv2, bts, sl)
+    kv2 = _bf(20, 128, 2, 128)  # 32 query heads per kv head are accepted
+    out, _ = torch.ops.npu.cascade_decode(_bf(16, 64, 128), kv2, kv2, btp, plen, kv2, kv2, bts, sl)
+    assert out.shape == (16, 64, 128)
     with pytest.raises(RuntimeError, match="cascade_decode: prefix and suffix pools"):
         torch.ops.npu.cascade_decode(q, kv, kv, btp, plen, _bf(20, 128, 4, 128), _bf(20, 128, 4, 128), bts, sl)

@@ -185,3 +185,81 @@ def test_catlass_fixture_lse_statistics(golden_dir):
     _, Lw = A.stage1(q, k, v, bt, qs, kvs, scale=1.0 / 128)
     assert abs(Lw.mean() - lse_g.mean()) > 0.03
     assert abs((L / np.log(2.0)).mean() - lse_g.mean()) > 1.0  # log2 instead of ln
+
+
+def test_tie_ambiguity_midpoint_far_and_band_edge():
+    """_tie_ambiguity: an ls sitting on a bf16 rounding midpoint is ambiguous by the
+    grid spacing there; an ls on the grid or a quarter-spacing away is not; the
+    band edge is tie_band_rel * ls (fa_fp32_ref.py:129-147, 195-200)."""
+    mid1 = 1.0 + 2.0 ** -8           # between 1 and 1 + 2^-7 (spacing 2^-7 in [1, 2))
+    mid2 = 0.3125 + 2.0 ** -10       # between 0.3125 and 0.3125 + 2^-9 (spacing in [0.25, 0.5))
+    mid3 = 3.0 + 2.0 ** -7           # between 3 and 3 + 2^-6
+    got = A._tie_ambiguity(np.array([mid1, mid2, mid3]), 2e-5)
+    assert np.array_equal(got, [2.0 ** -7, 2.0 ** -9, 2.0 ** -6])
+    far = np.array([1.0, 1.0 + 2.0 ** -9, 0.3125, 3.0 - 2.0 ** -8])
+    assert np.all(A._tie_ambiguity(far, 2e-5) == 0)
+    inside = mid1 * (1 - 1e-5)
+    outside = mid1 * (1 - 5e-5)
+    assert A._tie_ambiguity(np.array([inside]), 2e-5)[0] == 2.0 ** -7
+    assert A._tie_ambiguity(np.array([outside]), 2e-5)[0] == 0
+
+
+def _flip_closed_form(s, v, chunk, flips):
+    """O of one query row when the P elements in `flips` take the other bf16 neighbour
+    of exp(s - m) instead of the nearest one. Closed form of the chunked online
+    softmax: O = sum_i P_i v_i exp(m_c(i) - m_end) / sum_i exp(s_i - m_end), with
+    m_c the running max after chunk c; no recurrence shared with the oracle."""
+    n = len(s)
+    m_after = np.array([s[:min(n, (i // chunk + 1) * chunk)].max() for i in range(n)])
+    m_end = s.max()
+    ls = np.exp(s - m_after)
+    p = round_bf16(ls).astype(np.float64)
+    x32 = ls.astype(np.float32).view(np.uint32).astype(np.int64)
+    rne = (x32 + 0x7FFF + ((x32 >> 16) & 1)) & 0xFFFF0000
+    hi = ((rne + (1 << 16)) & 0xFFFFFFFF).astype(np.uint32).view(np.float32).astype(np.float64)
+    lo = ((rne - (1 << 16)) & 0xFFFFFFFF).astype(np.uint32).view(np.float32).astype(np.float64)
+    other = np.where(p < ls, hi, lo)
+    pp = np.where(flips, other, p)
+    gl = np.exp(s - m_end).sum()
+    return float((pp * v * np.exp(m_after - m_end)).sum() / gl)
+
+
+def test_stage1_tieband_bound_is_exact_over_all_flips():
+    """Brute force over every subset of rounding flips of a 6-token row in three
+    2-token chunks whose max moves twice: with V > 0 and every element ambiguous
+    (tie_band_rel = 1), A equals the spread max - min of the flipped outputs and
+    bounds each |O_flip - O|. The running-max decay of earlier chunks matters: the
+    accumulation sum_s dm_s X_s (each chunk scaled by its own step's decay only)
+    misses that spread, which is how the planted mistake is caught."""
+    import itertools
+    s = np.array([0.0, -1.0, 0.5, 0.2, 2.0, 1.0])
+    vv = np.array([1.0, 2.0, 0.5, 3.0, 1.5, 0.25])
+    k = np.zeros((1, 128, 1, 1))
+    v = np.zeros((1, 128, 1, 1))
+    k[0, :6, 0, 0] = s
+    v[0, :6, 0, 0] = vv
+    q = np.ones((1, 1, 1))
+    bt = np.zeros((1, 1), dtype=np.int32)
+    O, L, Amb = A.stage1_tieband(q, k, v, bt, [1], [6], chunk=2, tie_band_rel=1.0)
+    base = _flip_closed_form(s, vv, 2, np.zeros(6, bool))
+    assert abs(base - O[0, 0, 0]) < 1e-14
+    deltas = [_flip_closed_form(s, vv, 2, np.array(f, bool)) - base
+              for f in itertools.product([0, 1], repeat=6)]
+    spread = max(deltas) - min(deltas)
+    assert max(abs(d) for d in deltas) <= Amb[0, 0, 0] + 1e-15
+    assert abs(spread - Amb[0, 0, 0]) < 1e-14 * max(1.0, spread)
+    # planted mistake: each chunk's ambiguity scaled only by its own dm
+    m = -np.inf
+    gl, wrong = 0.0, 0.0
+    for c in range(3):
+        sc = s[2 * c:2 * c + 2]
+        m_new = max(m, sc.max())
+        dm = np.exp(m - m_new) if c else 1.0
+        ls = np.exp(sc - m_new)
+        gl = dm * gl + ls.sum()
+        wrong += dm * (A._tie_ambiguity(ls, 1.0) * vv[2 * c:2 * c + 2]).sum()
+        m = m_new
+    assert abs(wrong / gl - spread) > 1e-4
+    # with the reference's band (2e-5) none of these six is near a tie: A = 0
+    _, _, A0 = A.stage1_tieband(q, k, v, bt, [1], [6], chunk=2)
+    assert np.all(A0 == 0)

@@ -19,6 +19,13 @@ README.md:258). This module is that harness for the MI355X ops:
 
 The timing function is injectable (``timer=``) so the bucketing and caching logic
 is testable without a GPU.
+
+HIP-graph capture: measuring a bucket synchronises the device and creating the
+device-side prefix length copies from the host, and neither may happen while a
+stream is being captured. ``decode`` therefore raises during capture for a bucket
+without a decision and for a prefix length it has no device tensor for: measure
+(``choose``) or ``load_json`` the buckets, and make one eager call per prefix
+length (or pass ``prefix_len_tensor``), before capturing.
 """
 import json
 import math
@@ -49,6 +56,10 @@ def full_decode(query, key, value, prefix_block_table, prefix_len, suffix_block_
     bt = full_block_table(prefix_block_table, prefix_len // PAGE, suffix_block_table)
     kv = (suffix_kv_seqlens + prefix_len).contiguous()
     return torch.ops.npu.suffix_decode(query, key, value, bt, kv)
+
+
+def _capturing():
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
 
 
 def _bucket(batch, shared_len, shared_quantum):
@@ -89,6 +100,7 @@ class CascadeGate:
         self.timer = timer
         self.margin = margin  # cascade must be faster than full by this factor to be chosen
         self.decisions = {}   # (batch bucket, shared bucket) -> {"choice", "cascade_ms", "full_ms"}
+        self._plens = {}      # (device, prefix length) -> int64 [1] device tensor, made on first use
 
     # ---- buckets and decisions ---------------------------------------------------
     def bucket(self, batch, shared_len):
@@ -124,18 +136,44 @@ class CascadeGate:
         return c_ms, f_ms
 
     # ---- dispatch ---------------------------------------------------------------------
-    def decode(self, query, key, value, prefix_block_table, prefix_len, suffix_block_table, suffix_kv_seqlens):
+    def decode(self, query, key, value, prefix_block_table, prefix_len, suffix_block_table, suffix_kv_seqlens,
+               prefix_len_tensor=None):
         """Shared-prefix decode through the bucket's chosen form.
 
-        ``prefix_len`` is the host-side shared length (the bucketing key); the
-        device-side prefix length tensor the cascade needs is made from it.
+        ``prefix_len`` is the host-side shared length (the bucketing key). The
+        cascade's device-side prefix length is ``prefix_len_tensor`` when given,
+        else a tensor this gate makes once per (device, length) and reuses. A
+        prefix that is not page aligned always takes the cascade (the FULL form
+        needs whole prefix pages), without measuring.
         """
-        if self.choose(query.shape[0], prefix_len) == CASCADE or prefix_len % PAGE:
-            plen = torch.tensor([prefix_len], dtype=torch.int64, device=query.device)
+        if prefix_len % PAGE:
+            choice = CASCADE
+        else:
+            bk = self.bucket(query.shape[0], prefix_len)
+            if bk not in self.decisions and _capturing():
+                raise RuntimeError("CascadeGate.decode: bucket (batch %d, shared %d) has no decision and the "
+                                   "stream is being captured; measure it with choose() or load_json() before "
+                                   "capture" % bk)
+            choice = self.choose(query.shape[0], prefix_len)
+        if choice == CASCADE:
+            plen = prefix_len_tensor if prefix_len_tensor is not None else \
+                self._prefix_tensor(prefix_len, query.device)
             return torch.ops.npu.cascade_decode(query, key, value, prefix_block_table, plen, key, value,
                                                 suffix_block_table, suffix_kv_seqlens)
         return full_decode(query, key, value, prefix_block_table, prefix_len, suffix_block_table,
                            suffix_kv_seqlens)
+
+    def _prefix_tensor(self, prefix_len, device):
+        k = (str(device), int(prefix_len))
+        t = self._plens.get(k)
+        if t is None:
+            if _capturing():
+                raise RuntimeError("CascadeGate.decode: no device tensor for prefix length %d yet and the stream "
+                                   "is being captured; make one eager call with this length first, or pass "
+                                   "prefix_len_tensor" % prefix_len)
+            t = torch.tensor([int(prefix_len)], dtype=torch.int64, device=device)
+            self._plens[k] = t
+        return t
 
     # ---- persistence ------------------------------------------------------------------
     def to_json(self):

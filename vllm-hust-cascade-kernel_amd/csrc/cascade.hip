@@ -41,7 +41,7 @@ int cascade_layout(int64_t batch, int64_t num_heads, int64_t kv_heads, int64_t h
     if (batch < 0 || prefix_cap < 0 || suffix_cap < 0) return CK_E_INVALID_ARG;
     if (head_dim != kD) return CK_E_UNSUPPORTED;
     if (kv_heads <= 0 || num_heads <= 0 || num_heads % kv_heads != 0) return CK_E_INVALID_ARG;
-    if (num_heads / kv_heads > 8) return CK_E_UNSUPPORTED;
+    if (num_heads > (1 << 16)) return CK_E_INVALID_ARG;
     if (prefix_cap > ((int64_t)1 << 30) || suffix_cap > ((int64_t)1 << 30)) return CK_E_INVALID_ARG;
     const int64_t rows = batch * num_heads;
     int64_t s1 = 1, s1_ws = 0;

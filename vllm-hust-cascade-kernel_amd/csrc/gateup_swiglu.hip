@@ -563,7 +563,9 @@ __global__ __launch_bounds__(kSThreads) void gateup_skinny16_kernel(GemmArgs p) 
     }
 }
 
-// mode 3: d = workspace[:, :I] (epilogue-only rung), 8 columns per thread.
+// mode 3: d = workspace[:, :I] (epilogue-only rung), 8 columns per thread. The
+// workspace and d are 8-byte aligned (the ABI contract) and d_stride % 4 == 0,
+// so both sides move as two 8-byte words.
 __global__ __launch_bounds__(256) void gate_window_copy_kernel(const uint16_t *c, uint16_t *d, int64_t m,
                                                                int64_t n_half, int64_t d_stride) {
     const int64_t per_row = n_half / 8;
@@ -571,11 +573,11 @@ __global__ __launch_bounds__(256) void gate_window_copy_kernel(const uint16_t *c
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t r = i / per_row, q = i - r * per_row;
-        const uint4 v = *reinterpret_cast<const uint4 *>(c + r * 2 * n_half + q * 8);
-        uint16_t *dst = d + r * d_stride + q * 8;
-        // d_stride may be odd-aligned only to 8 bytes in general; store as 4 x 4 bytes
-        reinterpret_cast<uint2 *>(dst)[0] = make_uint2(v.x, v.y);
-        reinterpret_cast<uint2 *>(dst)[1] = make_uint2(v.z, v.w);
+        const uint2 *src = reinterpret_cast<const uint2 *>(c + r * 2 * n_half + q * 8);
+        const uint2 v0 = src[0], v1 = src[1];
+        uint2 *dst = reinterpret_cast<uint2 *>(d + r * d_stride + q * 8);
+        dst[0] = v0;
+        dst[1] = v1;
     }
 }
 

@@ -89,8 +89,8 @@ struct SuffixArgs {
     const int64_t *kv_seqlens;
     uint16_t *out;
     float *lse;
-    float *part_o;    // [kv_heads][chunks][2][G][kD]
-    float *part_lse;  // [kv_heads][chunks][2][G]
+    float *part_o;    // [kv head groups][chunks][2][G][kD]
+    float *part_lse;  // [kv head groups][chunks][2][G]
     int32_t *cw_out;  // [batch + 1] window prefix sums, written by workgroup 0
     int64_t bt_cols;
     int64_t num_blocks;
@@ -99,9 +99,10 @@ struct SuffixArgs {
     int64_t head_off;     // between kv heads:          128 (NHD) or 128 * 128 (BNSD)
     int batch;
     int num_heads;
-    int kv_heads;
+    int kv_heads;  // kv head groups of the grid: physical kv heads x kv_sub
+    int kv_sub;    // query-head groups per physical kv head (group = kv_sub x G)
     int kv_cap;
-    int chunks;  // workgroups per kv head
+    int chunks;  // workgroups per kv head group
     float scale_log2;
 };
 
@@ -206,8 +207,9 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
     const int lane = tid & 63;
     const int t = lane >> 3;  // token slot of this lane in the wave's 8 tokens
     const int c = lane & 7;   // column pair: dims 8c.. and 64+8c..
-    const int g = blockIdx.x % a.kv_heads;
+    const int g = blockIdx.x % a.kv_heads;  // kv head group: query heads g * G .. + G
     const int chunk = blockIdx.x / a.kv_heads;
+    const int gk = g / a.kv_sub;            // the physical kv head they read
     CK_LDS float *pw = (CK_LDS float *)(smem + kPwOff) + wid * 8 * kPwRow;
 
     // ---- lengths and window prefix sums (4 sequences per thread, block scan) ------
@@ -283,7 +285,7 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
         }
         int page = pgring[n % kPgRing];
         if (page < 0 || (int64_t)page >= a.num_blocks) page = 0;  // rows ignored at use
-        const int64_t pbase = (int64_t)page * a.page_stride + (int64_t)g * a.head_off + (lane & 15) * 8;
+        const int64_t pbase = (int64_t)page * a.page_stride + (int64_t)gk * a.head_off + (lane & 15) * 8;
         const int t0 = (cur.k * kWin) % kPage + (lane >> 4);
 #pragma unroll
         for (int j = 0; j < kKvDmaPerWave / 2; ++j) {
@@ -608,15 +610,15 @@ struct EpilogueArgs {
     Stage1Result s1;
     const uint16_t *o2;     // bf16 [nb][H][kD] whole-sequence suffix results
     const float *lse2;      // [nb * H]
-    const float *part_o;    // suffix partials [kv_heads][chunks][2][G][kD]
-    const float *part_lse;  // [kv_heads][chunks][2][G]
+    const float *part_o;    // suffix partials [kv head groups][chunks][2][G][kD]
+    const float *part_lse;  // [kv head groups][chunks][2][G]
     const int32_t *cw;      // [nb + 1] window prefix sums of the group
     uint16_t *out;          // bf16 [batch][H][kD]
     float *lse_out;         // [batch * H]
     int64_t b0;
     int nb;
     int num_heads;
-    int kv_heads;
+    int kv_heads;  // kv head groups, as in SuffixArgs
     int chunks;
 };
 
@@ -735,9 +737,9 @@ __global__ __launch_bounds__(kMaxGroup * 32) void cascade_epilogue_kernel(Epilog
 
 int64_t ceil_div(int64_t x, int64_t y) { return (x + y - 1) / y; }
 
-int64_t group_parts(int64_t num_heads, int64_t kv_heads, int64_t chunks) {
-    return kv_heads * chunks * 2 * (num_heads / kv_heads);
-}
+// partial (O, LSE) slots: 2 per (query head, chunk) -- the same count for any
+// split of the heads into kv head groups
+int64_t group_parts(int64_t num_heads, int64_t chunks) { return num_heads * chunks * 2; }
 
 template <int G>
 int launch_suffix(const SuffixArgs &a, bool fixup, const EpilogueArgs *epi, hipStream_t st) {
@@ -761,13 +763,23 @@ int check_suffix_dims(int64_t batch, int64_t num_heads, int64_t kv_heads, int64_
     if (batch < 0 || kv_cap < 0) return CK_E_INVALID_ARG;
     if (head_dim != kD) return CK_E_UNSUPPORTED;
     if (kv_heads <= 0 || num_heads <= 0 || num_heads % kv_heads != 0) return CK_E_INVALID_ARG;
-    const int64_t group = num_heads / kv_heads;
-    if (group > kMaxGroup) return CK_E_UNSUPPORTED;
+    if (num_heads > (1 << 16)) return CK_E_INVALID_ARG;
     if (kv_cap > (int64_t)1 << 30) return CK_E_INVALID_ARG;
     return CK_OK;
 }
 
 }  // namespace
+
+// Query-head groups per kv head: a GQA group of more than kMaxGroup heads is
+// split into the fewest equal groups of at most kMaxGroup heads. Each group is
+// streamed as if it had its own kv head (the kernel reads the shared physical
+// head), so the kernels keep their per-head registers bounded for any group.
+int64_t suffix_sub_groups(int64_t num_heads, int64_t kv_heads) {
+    const int64_t group = num_heads / kv_heads;
+    for (int64_t n = (group + kMaxGroup - 1) / kMaxGroup; n < group; ++n)
+        if (group % n == 0) return n;
+    return group;
+}
 
 // Sequences per stream-kernel launch: the window/length prefix sums live in
 // LDS (kMaxBatch entries) and must stay below 2^31 tokens.
@@ -778,19 +790,20 @@ int64_t suffix_group_batch(int64_t kv_cap) {
     return n < 1 ? 1 : n;
 }
 
-// Workgroups per kv head: the grid holds as many workgroups as can be resident
+// Workgroups per kv head group: the grid holds as many workgroups as can be resident
 // at once. Up to 5 query heads per kv head the stream kernel fits in 128 VGPRs
 // and kBlocksPerCu workgroups share a CU; 6-8 heads need more registers (the
 // per-head accumulators) and run one per CU, where a grid twice that size
 // would queue half its workgroups behind the first half.
 int64_t suffix_default_chunks(int64_t num_heads, int64_t kv_heads) {
-    const int64_t per_cu = num_heads / kv_heads <= 5 ? kBlocksPerCu : 1;
-    const int64_t p = per_cu * 256 / kv_heads;
+    const int64_t groups = kv_heads * suffix_sub_groups(num_heads, kv_heads);
+    const int64_t per_cu = num_heads / groups <= 5 ? kBlocksPerCu : 1;
+    const int64_t p = per_cu * 256 / groups;
     return p > 0 ? p : 1;
 }
 
 int64_t suffix_group_ws_bytes(int64_t nb, int64_t num_heads, int64_t kv_heads, int64_t chunks) {
-    const int64_t parts = group_parts(num_heads, kv_heads, chunks);
+    const int64_t parts = group_parts(num_heads, chunks);
     return parts * (kD + 1) * (int64_t)sizeof(float) + (nb + 1) * (int64_t)sizeof(int32_t) + 256;
 }
 
@@ -799,8 +812,9 @@ int suffix_launch_group(const void *q, const void *k, const void *v, const int32
                         int64_t num_blocks, int64_t kv_layout, float scale, int64_t kv_cap, int64_t chunks,
                         void *out, float *lse, void *group_ws, const Stage1Result *cascade, void *final_out,
                         float *final_lse, hipStream_t stream) {
-    const int64_t group = num_heads / kv_heads;
-    const int64_t parts = group_parts(num_heads, kv_heads, chunks);
+    const int64_t sub = suffix_sub_groups(num_heads, kv_heads);
+    const int64_t G = num_heads / kv_heads / sub;  // query heads per workgroup
+    const int64_t parts = group_parts(num_heads, chunks);
     SuffixArgs a;
     a.q = static_cast<const uint16_t *>(q) + b0 * num_heads * kD;
     a.k = static_cast<const uint16_t *>(k);
@@ -819,7 +833,8 @@ int suffix_launch_group(const void *q, const void *k, const void *v, const int32
     a.head_off = kv_layout == CK_KV_BNSD ? (int64_t)kPage * kD : kD;
     a.batch = (int)nb;
     a.num_heads = (int)num_heads;
-    a.kv_heads = (int)kv_heads;
+    a.kv_heads = (int)(kv_heads * sub);
+    a.kv_sub = (int)sub;
     a.kv_cap = (int)kv_cap;
     a.chunks = (int)chunks;
     a.scale_log2 = scale * kLog2e;
@@ -836,12 +851,12 @@ int suffix_launch_group(const void *q, const void *k, const void *v, const int32
         e.b0 = b0;
         e.nb = (int)nb;
         e.num_heads = (int)num_heads;
-        e.kv_heads = (int)kv_heads;
+        e.kv_heads = a.kv_heads;
         e.chunks = (int)chunks;
     }
     const bool fixup = cascade == nullptr;
     const EpilogueArgs *ep = cascade ? &e : nullptr;
-    switch (group) {
+    switch (G) {
         case 1: return launch_suffix<1>(a, fixup, ep, stream);
         case 2: return launch_suffix<2>(a, fixup, ep, stream);
         case 3: return launch_suffix<3>(a, fixup, ep, stream);
@@ -881,12 +896,14 @@ extern "C" int ck_suffix_decode(const void *q, const void *k, const void *v, con
     if (bt_cols < 0 || num_blocks < 0 || kv_cap > bt_cols * kPage) return CK_E_INVALID_ARG;
     if (batch == 0) return CK_OK;
     if (!q || !k || !v || !block_table || !kv_seqlens || !out || !lse) return CK_E_NULL_PTR;
-    // q/k/v rows and the workspace partials move up to 16 bytes per lane
-    if (!aligned_to(q, 16) || !aligned_to(k, 16) || !aligned_to(v, 16) || !aligned_to(out, 4) ||
+    // q/k/v rows and the workspace partials move up to 16 bytes per lane; the
+    // fix-up kernel stores bf16 O four elements (8 bytes) at a time
+    if (!aligned_to(q, 16) || !aligned_to(k, 16) || !aligned_to(v, 16) || !aligned_to(out, 8) ||
         !aligned_to(lse, 4) || !aligned_to(workspace, 16))
         return CK_E_INVALID_ARG;
     const int64_t chunks = num_splits > 0 ? num_splits : suffix_default_chunks(num_heads, kv_heads);
-    if (kv_heads * chunks > 0x7FFFFFFF || chunks > (1 << 20)) return CK_E_INVALID_ARG;
+    if (kv_heads * suffix_sub_groups(num_heads, kv_heads) * chunks > 0x7FFFFFFF || chunks > (1 << 20))
+        return CK_E_INVALID_ARG;
     const int64_t per_launch = suffix_group_batch(kv_cap);
     const int64_t nbmax = batch < per_launch ? batch : per_launch;
     if (workspace == nullptr || workspace_bytes < suffix_group_ws_bytes(nbmax, num_heads, kv_heads, chunks))

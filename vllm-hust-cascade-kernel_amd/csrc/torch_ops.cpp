@@ -260,7 +260,6 @@ std::tuple<at::Tensor, at::Tensor> suffix_decode_impl(const at::Tensor &query, c
     TORCH_CHECK(embed == 128 && key.size(3) == 128, "suffix_decode: only head dim 128 is supported");
     TORCH_CHECK(block_size == 128, "suffix_decode: only paged blockSize 128 is supported");
     TORCH_CHECK(kv_heads > 0 && num_heads % kv_heads == 0, "suffix_decode: numHeads must be a multiple of kvHeads");
-    TORCH_CHECK(num_heads / kv_heads <= 8, "suffix_decode: at most 8 query heads per kv head are supported");
     auto out = at::empty({batch, num_heads, embed}, query.options());
     auto lse = at::empty({batch * num_heads}, query.options().dtype(at::kFloat));
     if (batch == 0 || query.device().is_meta()) return {out, lse};
@@ -327,7 +326,6 @@ std::tuple<at::Tensor, at::Tensor> cascade_decode_impl(const at::Tensor &query, 
     TORCH_CHECK(prefix_key.size(1) == 128 && suffix_key.size(sfx_bnsd ? 2 : 1) == 128,
                 "cascade_decode: only paged blockSize 128 is supported");
     TORCH_CHECK(kv_heads > 0 && num_heads % kv_heads == 0, "cascade_decode: numHeads must be a multiple of kvHeads");
-    TORCH_CHECK(num_heads / kv_heads <= 8, "cascade_decode: at most 8 query heads per kv head are supported");
     for (const at::Tensor *t : {&prefix_key, &prefix_value, &prefix_block_table, &prefix_kv_seqlens, &suffix_key,
                                 &suffix_value, &suffix_block_table, &suffix_kv_seqlens})
         TORCH_CHECK(t->device() == query.device(), "cascade_decode: all tensors must be on the same HIP device");
