@@ -54,6 +54,7 @@ extern "C" {
 #define CK_E_NULL_PTR (-2)      /* a required pointer is NULL */
 #define CK_E_WORKSPACE (-3)     /* workspace missing or smaller than the plan requires */
 #define CK_E_UNSUPPORTED (-4)   /* shape supported by the API but not by a built kernel */
+#define CK_E_SCRATCH_LIMIT (-5) /* more workspace than ck_cascade_decode_noalloc's scratch holds */
 
 /* Human-readable text for a code returned by any ck_* function. */
 const char *ck_error_string(int code);
@@ -193,6 +194,30 @@ int ck_cascade_decode(const void *q, const void *prefix_k, const void *prefix_v,
                       int64_t num_heads, int64_t kv_heads, int64_t head_dim, int64_t block_size,
                       float scale, int64_t prefix_cap, int64_t suffix_cap, void *out, float *lse_out,
                       void *workspace, int64_t workspace_bytes, void *stream);
+
+/* ============================================================================
+ * ck_cascade_decode without a workspace argument, for callers that cannot
+ * allocate (code under HIP-graph capture, serving loops that forbid
+ * allocation). No counterpart in the reference. Arguments and results are
+ * those of ck_cascade_decode; the workspace is a device array inside this
+ * library, 32 MiB per GPU (CK_CASCADE_NOALLOC_SCRATCH_BYTES), held by every GPU
+ * the library runs on until the process ends. A shape whose
+ * ck_cascade_decode_plan exceeds it is refused with CK_E_SCRATCH_LIMIT before
+ * anything is launched. The call allocates and frees nothing. All calls on one
+ * GPU share its array: calls that overlap on one GPU (other streams, other
+ * threads) race and must be serialised by the caller.
+ * ========================================================================== */
+#define CK_CASCADE_NOALLOC_SCRATCH_BYTES (32ll << 20)
+
+int ck_cascade_decode_noalloc(const void *q, const void *prefix_k, const void *prefix_v,
+                              const int32_t *prefix_block_table, int64_t prefix_bt_cols,
+                              const int64_t *prefix_kv_seqlen, int64_t prefix_num_blocks, const void *suffix_k,
+                              const void *suffix_v, const int32_t *suffix_block_table, int64_t suffix_bt_cols,
+                              const int64_t *suffix_kv_seqlens, int64_t suffix_num_blocks,
+                              int64_t suffix_kv_layout, int64_t batch,
+                              int64_t num_heads, int64_t kv_heads, int64_t head_dim, int64_t block_size,
+                              float scale, int64_t prefix_cap, int64_t suffix_cap, void *out, float *lse_out,
+                              void *stream);
 
 /* ============================================================================
  * gate_up GEMM with the epilogue ladder of OPS/f3_floor (bf16, fp32 accumulate).

@@ -35,12 +35,16 @@ SIGNATURES = {
     "ck_cascade_decode_plan": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _p64]),
     "ck_cascade_decode": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
                                  _i64, _i64, _i64, _i64, _f32, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
+    "ck_cascade_decode_noalloc": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64,
+                                         _i64, _i64, _i64, _i64, _i64, _f32, _i64, _i64, _vp, _vp, _vp]),
     "ck_add_rms_norm_stats": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _int, _i64, _f64, _vp]),
 }
 
 CK_DTYPE_BF16 = 0
 CK_DTYPE_F32 = 1
 CK_DTYPE_F16 = 2
+CK_E_SCRATCH_LIMIT = -5
+CASCADE_NOALLOC_SCRATCH_BYTES = 32 << 20
 CK_KV_NHD = 0
 CK_KV_BNSD = 1
 

@@ -8,6 +8,8 @@ extern "C" const char *ck_error_string(int code) {
         case CK_E_NULL_PTR: return "a required pointer is NULL";
         case CK_E_WORKSPACE: return "workspace missing or smaller than the plan requires";
         case CK_E_UNSUPPORTED: return "shape not supported by the built kernels";
+        case CK_E_SCRATCH_LIMIT:
+            return "the call needs more workspace than the no-allocation entry point's device scratch holds";
         default: break;
     }
     if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

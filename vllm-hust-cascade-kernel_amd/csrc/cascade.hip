@@ -16,8 +16,25 @@
 //      final bf16 O and the merged LSE.
 // Three launches instead of five (stage-1, combine, suffix, fix-up, merge),
 // and neither partial result makes an extra round trip through HBM.
+//
+// ck_cascade_decode_noalloc is the same call for callers that cannot allocate
+// (code under HIP-graph capture, serving loops that forbid allocation): its
+// workspace is `scratch`, a file-scope device array of kScratchBytes that
+// every GPU the library runs on holds until the process ends. Host code never
+// passes the array's name to a kernel (on the host it is only a stand-in
+// symbol): the device address comes from hipGetSymbolAddress, looked up once
+// per device with that device current. Calls on one GPU share its array, so
+// calls that overlap on one GPU race. Nothing in it has to start at zero:
+// every workspace word a kernel reads was written earlier in the same call.
+#include <atomic>
+
 #include "ck_common.h"
 #include "ck_internal.h"
+
+// The no-allocation entry point's workspace (32 MiB: the cascade at BASELINE
+// config 2 plans 19.6 MB, config 5 23.3 MB).
+constexpr int64_t kScratchBytes = CK_CASCADE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kScratchBytes];
 
 namespace {
 
@@ -136,4 +153,55 @@ extern "C" int ck_cascade_decode(const void *q, const void *prefix_k, const void
         if (rc != CK_OK) return rc;
     }
     return CK_OK;
+}
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<void *> g_scratch[kMaxDevices];
+
+// Device address of `scratch` on the current device, looked up on the first
+// call per device and kept (every GPU holds its own copy at its own address).
+int scratch_address(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (dev < 0 || dev >= kMaxDevices) return CK_E_UNSUPPORTED;
+    void *p = g_scratch[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return static_cast<int>(e);
+        if (p == nullptr) return static_cast<int>(hipErrorInvalidSymbol);
+        g_scratch[dev].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return CK_OK;
+}
+
+}  // namespace
+
+extern "C" int ck_cascade_decode_noalloc(const void *q, const void *prefix_k, const void *prefix_v,
+                                         const int32_t *prefix_block_table, int64_t prefix_bt_cols,
+                                         const int64_t *prefix_kv_seqlen, int64_t prefix_num_blocks,
+                                         const void *suffix_k, const void *suffix_v,
+                                         const int32_t *suffix_block_table, int64_t suffix_bt_cols,
+                                         const int64_t *suffix_kv_seqlens, int64_t suffix_num_blocks,
+                                         int64_t suffix_kv_layout, int64_t batch, int64_t num_heads,
+                                         int64_t kv_heads, int64_t head_dim, int64_t block_size, float scale,
+                                         int64_t prefix_cap, int64_t suffix_cap, void *out, float *lse_out,
+                                         void *stream) {
+    CascadeLayout L;
+    int rc = cascade_layout(batch, num_heads, kv_heads, head_dim, prefix_cap, suffix_cap, &L);
+    if (rc != CK_OK) return rc;
+    if (L.total > kScratchBytes) return CK_E_SCRATCH_LIMIT;
+    void *ws = nullptr;
+    if (L.total > 0) {
+        rc = scratch_address(&ws);
+        if (rc != CK_OK) return rc;
+    }
+    return ck_cascade_decode(q, prefix_k, prefix_v, prefix_block_table, prefix_bt_cols, prefix_kv_seqlen,
+                             prefix_num_blocks, suffix_k, suffix_v, suffix_block_table, suffix_bt_cols,
+                             suffix_kv_seqlens, suffix_num_blocks, suffix_kv_layout, batch, num_heads, kv_heads,
+                             head_dim, block_size, scale, prefix_cap, suffix_cap, out, lse_out, ws,
+                             L.total > 0 ? kScratchBytes : 0, stream);
 }
