@@ -112,6 +112,46 @@ def test_precision_suite(case, share, seed):
     assert np.array_equal(lse_d.view(np.uint32), lse_f.view(np.uint32))
 
 
+# Cases whose every kv length fits one 64-token tile: the kernel's running max is
+# then the whole row's max, which is also the reference's 512-column chunk max, so
+# the kernel and the reference round P on the same grid and the reference's own
+# gate applies (run_precision_suite.py:80-89): |O - O_ref| <= A + 3e-6, with A the
+# near-tie bound of stage1_tieband, and LSE within 1e-3.
+TIEBAND = [("min_b1_kv64", 1, [64], 40, 8, 1), ("b64_kv64", 64, [64] * 64, 40, 8, 1),
+           ("varlen_b5_kv_le64", 5, [1, 17, 33, 50, 64], 40, 8, 1), ("flat_T64_kv64", 1, [64], 40, 8, 64)]
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+@pytest.mark.parametrize("case", TIEBAND, ids=[c[0] for c in TIEBAND])
+def test_reference_tieband_gate_one_tile(case, seed):
+    name, batch, kvs, H, KVH, q_len = case
+    inp = paged_inputs(batch, kvs, H, KVH, seed=seed, q_len=q_len, share_blocks=False, permute=True)
+    out, lse = _run(inp, q_len)
+    T = inp["num_tokens"]
+    L, _ = A.unpack_lse(lse, T, H)
+    O_ref, L_ref, amb = A.stage1_tieband(inp["q"], inp["k"], inp["v"], inp["block_table"], inp["q_seqlens"],
+                                         inp["kv_seqlens"])
+    err = np.abs(out.astype(np.float64) - O_ref)
+    bound = amb + 3e-6
+    # recorded as the largest fraction of its own bound any element uses
+    record_margin("stage1 tie-band gate %s seed%d" % (name, seed), (err / bound).max(), 1.0)
+    assert np.all(err <= bound), (err - bound).max()
+    assert np.abs(L.astype(np.float64) - L_ref).max() <= 1e-3
+
+
+# More than 128 query rows per kv head with enough kv to fill the chip: the
+# 256-row (8-wave) workgroups, with partial last tiles and varlen requests
+WIDE = [("wide_flat_T64_h64_kv32718", 1, [32718], 64, 8, 64), ("wide_req2_q64_varlen", 2, [30001, 19999], 64, 8, 64)]
+
+
+@pytest.mark.parametrize("case", WIDE, ids=[c[0] for c in WIDE])
+def test_wide_row_tiles(case):
+    name, batch, kvs, H, KVH, q_len = case
+    inp = paged_inputs(batch, kvs, H, KVH, seed=11, q_len=q_len, permute=True)
+    out, lse = _run(inp, q_len)
+    _check(inp, out, lse, H, name)
+
+
 # test_lse_flatten_regression.py:30-47: B=1 flattened form, q_len = T
 FLAT = [("flat_T64_kv128", 64, 40, 8, 128), ("flat_T64_kv4356", 64, 40, 8, 4356),
         ("flat_T8_3b", 8, 16, 2, 4096), ("flat_T17_bnd", 17, 40, 8, 4096), ("flat_T63_odd", 63, 40, 8, 4096)]

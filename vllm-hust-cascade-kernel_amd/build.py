@@ -46,9 +46,16 @@ def run(cmd, cwd=None):
     return out
 
 
+# Per-source code-generation options. The stage-1 kernel keeps its score and
+# output accumulators in architectural VGPRs (MFMA results written there, not
+# to AGPRs): the softmax reads and rescales them with VALU instructions every
+# 128 tokens, and AGPR-resident accumulators cost a copy in and out each time.
+SOURCE_FLAGS = {"fa_stage1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def compile_hip(src):
     obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
-    run([HIPCC] + HIP_FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj])
+    run([HIPCC] + HIP_FLAGS + SOURCE_FLAGS.get(src, []) + ["-c", os.path.join(CSRC, src), "-o", obj])
     return obj
 
 

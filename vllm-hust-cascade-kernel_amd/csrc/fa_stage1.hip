@@ -12,23 +12,28 @@
 //   op_host/fa_fp32_stage1.cpp:238).
 //
 // MI355X design (not a translation of the AIC/AIV pipeline):
-// * Work item = (request b, kv head g, m-tile of 128 query rows, kv split).
+// * Work item = (request b, kv head g, m-tile of query rows, kv split).
 //   Query rows of one kv head are token-major (row r -> token r / group,
 //   head g*group + r % group), so the GQA group and every query of the request
 //   that shares the prefix ride in the same MFMA tile: the flattened cascade
 //   form (one request, q_len = batch) reads each prefix page once per m-tile.
-// * One workgroup = 128 query rows x one kv split, run by 8 waves: wave w owns
-//   query rows 32*(w%4) .. +32 and token half w/4 of every 64-token tile, with
-//   its own online-softmax state; the two halves merge through LDS at the end.
-//   Two waves per SIMD let one wave's softmax VALU overlap the other's MFMAs.
-//   K and V tiles stream into a 4-slot LDS ring (4 x 32 KB) by global->LDS DMA
-//   (global_load_lds, 16 B per lane): no staging registers. Tiles go in pairs:
-//   a pair is computed while the next pair lands, with one barrier, one
-//   running-max update and at most one O rescale per pair (the rescale, 64
-//   multiplies per lane, is the largest VALU item of a tile). The split's page
-//   ids are read once into LDS, so no load in the loop depends on another
-//   load. Each wave keeps its Q rows as MFMA operands in registers for the
-//   whole kv loop.
+// * Every wave owns 32 query rows and all tokens of them, so a row has one
+//   online-softmax state over the whole split and P is rounded on the row's
+//   own running maximum (moved once per 64-token tile; for kv <= 64 that is
+//   the row maximum the reference rounds on). Two kernels:
+//   - stage1_tile_kernel (m-tile of 128 rows): 4 waves, one per SIMD with 512
+//     registers. Iteration t runs the QK MFMAs of tile t + 1 and the PV MFMAs
+//     of tile t in a fixed issue order, with one slice of tile t's softmax
+//     and, every four MFMAs, one of the wave's DMAs between them. K and V
+//     stream through separate 3-slot LDS rings (K one tile ahead of V).
+//   - stage1_wide_kernel (m-tile of 256 rows, when a request has more than 128
+//     rows per kv head and enough kv to fill the chip): 8 waves, two per SIMD;
+//     every 64-token K/V tile in LDS feeds 256 rows, and one wave of a SIMD
+//     issues MFMAs while the other waits on reads or runs its softmax.
+//   K/V tiles land by global->LDS DMA (global_load_lds, 16 B per lane; no
+//   staging registers); the split's page ids are read once into LDS, so no
+//   load in the loop depends on another load. Q stays in registers as MFMA
+//   operands for the whole kv loop.
 // * S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (A = K rows from LDS, B = Q); the
 //   accumulator layout puts one query row per lane, so row max / row sum need a
 //   single cross-half exchange. P^T leaves the accumulator directly as the B
@@ -41,18 +46,15 @@
 //   consecutive tokens swz is a bijection (fragment reads: 16 rows, one chunk,
 //   16 distinct bank groups), and over 4 consecutive tokens it differs in bits
 //   2-3 (transpose reads: 4 rows x 4 chunks of one 64-byte group land in 16
-//   distinct bank groups). Both read kinds are bank-conflict free; the plain
-//   t & 15 swizzle leaves the transpose reads 4-way conflicted.
+//   distinct bank groups). Both read kinds are bank-conflict free.
 // * Softmax runs in the log2 domain (p = exp2(s * scale * log2(e) - m), one
 //   FMA and one exp2 per score); LSE is converted back to natural log.
-// * The epilogue merges the two token halves through LDS and re-lays O out as
-//   whole rows, so each global store writes two contiguous 512-byte rows
-//   (lane-per-row stores of the accumulator layout scatter 32-byte pieces and
-//   run at a fraction of the write bandwidth).
+// * The epilogue re-lays O out as whole rows through the idle rings, so each
+//   global store writes two contiguous 512-byte rows.
 // * Split-KV fills the chip when batch*kv_heads*m-tiles is small; partial
 //   (O, LSE) pairs are folded by an N-way LSE merge (stage1_combine_kernel).
 // * Block order is XCD-aware: the m-tiles that read the same kv pages are
-//   placed on the same XCD so the second read hits that XCD's L2.
+//   placed on the same XCD so the later reads hit that XCD's L2.
 #include <cmath>
 
 #include "ck_common.h"
@@ -63,16 +65,7 @@ namespace {
 
 constexpr int kD = 128;          // head dim (op contract)
 constexpr int kPage = 128;       // paged block size (op contract)
-constexpr int kTileN = 64;       // kv tokens per tile
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * kWave;
-constexpr int kRows = 128;          // query rows per workgroup (4 row blocks x 2 token halves)
-constexpr int kStages = 4;          // LDS ring depth
-constexpr int kTileBytes = kTileN * kD * 2;   // 16 KB for K, the same for V
-constexpr int kStageBytes = 2 * kTileBytes;
-constexpr int kMaxSplitPages = 256;           // page ids held in LDS per split
-constexpr int kLdsBytes = kStages * kStageBytes + kMaxSplitPages * 4;
-constexpr int kDmaPerTile = 2 * (kTileBytes / 1024) / kWaves;  // 16-B-per-lane DMAs per wave per tile (4)
+constexpr int kMaxSplitPages = 256;   // page ids held in LDS per split
 
 struct Stage1Args {
     const uint16_t *q;
@@ -114,17 +107,45 @@ __device__ __forceinline__ bf16x8 pack_p(const f32x16 &s, int base) {
 __device__ __forceinline__ int tile_swz(int tok) { return ((tok & 3) << 2) | ((tok >> 2) & 3); }
 __device__ __forceinline__ int tile_off(int tok, int c) { return tok * (kD * 2) + ((c ^ tile_swz(tok)) << 4); }
 
-__global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
+// Software-pipelined whole-row kernel. 4 waves (one per SIMD, 512 registers
+// each); wave w owns RB blocks of 32 query rows (rows 32 RB w .. + 32 RB of the
+// workgroup's 128 RB) and every token of them, so each row has one
+// online-softmax state and P is rounded on the row's own running maximum,
+// which moves once per 64-token tile. Every K or V fragment read from LDS
+// feeds RB MFMAs (RB = 2 halves the LDS bytes per MFMA).
+// Iteration t runs the QK MFMAs of tile t + 1 and the PV MFMAs of tile t in a
+// fixed order, with one slice of tile t's softmax and, every few MFMAs, one of
+// the wave's 8 DMAs of the tile two ahead between them: the wave issues its
+// VALU work and DMAs while the matrix pipe is busy. K and V stream through
+// separate 3-slot LDS rings (K is read one iteration before V), so every DMA
+// is issued two iterations before its first reader. Past the last tile the
+// DMAs repeat into slots nobody reads again, so every iteration issues the
+// same number and the vmcnt wait is exact.
+constexpr int kTW = 4;                               // waves per workgroup
+constexpr int kTTok = 64;                            // tokens per tile
+constexpr int kTBytes = kTTok * kD * 2;              // 16 KB of K (or V) per tile
+constexpr int kTSlots = 3;                           // ring depth of each of K and V
+constexpr int kTBlk = kTBytes / 1024 / kTW;          // 1-KB DMAs of K (and of V) per wave per tile
+constexpr int kTDma = 2 * kTBlk;                     // DMAs per wave per tile
+constexpr int kTLds = 2 * kTSlots * kTBytes + kMaxSplitPages * 4;
+
+template <int RB>
+__global__ __launch_bounds__(kTW * 64) void stage1_tile_kernel(Stage1Args a) {
+    constexpr int kRowsWg = kTW * 32 * RB;
+    // the epilogue parks every row block's 16 KB of O in the (idle) rings; RB = 2
+    // would also need more than a wave's 512 registers (it spills), so the
+    // launcher instantiates RB = 1 only
+    static_assert(kTW * RB * 32 * kD * 4 <= 2 * kTSlots * kTBytes, "epilogue slabs fit the rings");
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
     CK_LDS char *smem = (CK_LDS char *)smem_raw;
-    CK_LDS int *s_pages = (CK_LDS int *)(smem + kStages * kStageBytes);
+    CK_LDS char *kring = smem;
+    CK_LDS char *vring = smem + kTSlots * kTBytes;
+    CK_LDS int *s_pages = (CK_LDS int *)(smem + 2 * kTSlots * kTBytes);
 
     const int tid = threadIdx.x;
     const int wid = tid >> 6;
     const int lane = tid & 63;
     const int hh = lane >> 5;
-    const int rb = wid & 3;   // row block
-    const int th = wid >> 2;  // token half of each tile
 
     uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
     const int mt = w % a.mtiles;
@@ -143,18 +164,471 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
         qs = a.q_start[b];
     }
     const int rows_b = qlen * a.group;
-    const int row0 = mt * kRows;
+    const int row0 = mt * kRowsWg;
     if (row0 >= rows_b) return;  // uniform over the workgroup
 
-    const int wrow0 = row0 + rb * 32;
+    const int wrow0 = row0 + wid * 32 * RB;
+    const bool wave_active = wrow0 < rows_b;
+    int64_t qrow[RB];
+    bool row_valid[RB];
+    bf16x8 qf[RB][8];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int r = wrow0 + rb * 32 + (lane & 31);
+        row_valid[rb] = r < rows_b;
+        const int t_local = r / a.group;
+        const int h = g * a.group + (r - t_local * a.group);
+        qrow[rb] = (int64_t)(qs + t_local) * a.num_heads + h;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+            if (row_valid[rb]) {
+                qf[rb][kk] = *reinterpret_cast<const bf16x8 *>(a.q + qrow[rb] * kD + 16 * kk + 8 * hh);
+            } else {
+                qf[rb][kk] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+            }
+        }
+    }
+    const int kv_lo = sp * a.split_len;  // a multiple of the page size
+    {
+        const int pg0 = kv_lo / kPage;
+        const int64_t avail = a.bt_cols - pg0;
+        const int pg_n = (int)min((int64_t)(a.split_len / kPage), avail > 0 ? avail : (int64_t)0);
+        for (int pi = tid; pi < pg_n; pi += kTW * 64) {
+            const int page = a.bt[(int64_t)b * a.bt_cols + pg0 + pi];
+            s_pages[pi] = (page >= 0 && (int64_t)page < a.num_blocks) ? page : -1;
+        }
+    }
+    int64_t kvl = a.kv_seqlens[b];
+    const int64_t kv_lim = a.bt_cols * kPage;
+    if (kvl > kv_lim) kvl = kv_lim;
+    if (kvl > a.kv_cap) kvl = a.kv_cap;
+    if (kvl < 0 || a.num_blocks <= 0) kvl = 0;
+    int kv_hi = kv_lo + a.split_len;
+    if (kv_hi > (int)kvl) kv_hi = (int)kvl;
+    const int ntok = kv_hi > kv_lo ? kv_hi - kv_lo : 0;
+    const int ntiles = (ntok + kTTok - 1) / kTTok;
+
+    wait_vmcnt<0>();
+    __syncthreads();  // s_pages visible
+
+    // DMA geometry: one wave instruction moves 4 token rows (1 KB); lane ->
+    // token 4 blk + lane / 16 and LDS chunk lane % 16, which holds global chunk
+    // (lane % 16) ^ tile_swz(token). Per-lane element offsets inside a tile.
+    const int64_t head_stride = (int64_t)a.kv_heads * kD;
+    uint32_t dma_off[kTBlk];
+#pragma unroll
+    for (int j = 0; j < kTBlk; ++j) {
+        const int tt = (wid * kTBlk + j) * 4 + (lane >> 4);
+        dma_off[j] = (uint32_t)(tt * head_stride + g * kD + (((lane & 15) ^ tile_swz(tt)) << 3));
+    }
+    // DMA j (0 .. kTDma-1: K blocks, then V blocks) of the wave's share of tile
+    // t (K) or tile t - 1 (V) -- the two the iteration before t prefetches. A
+    // tile past the end repeats the last tile into its own (dead) slot.
+    auto tile_src = [&](int t) {  // called only when ntiles > 0
+        const int tc = t < ntiles ? t : ntiles - 1;
+        const int raw = __builtin_amdgcn_readfirstlane(s_pages[tc >> 1]);
+        const int64_t tok0 = (int64_t)(raw < 0 ? 0 : raw) * kPage + (tc & 1) * kTTok;
+        return tok0 * head_stride;
+    };
+    auto dma_k = [&](int t, int j) {
+        dma16(a.k + tile_src(t) + dma_off[j], kring + (t % kTSlots) * kTBytes + (wid * kTBlk + j) * 1024);
+    };
+    auto dma_v = [&](int t, int j) {
+        dma16(a.v + tile_src(t) + dma_off[j], vring + (t % kTSlots) * kTBytes + (wid * kTBlk + j) * 1024);
+    };
+    // the iteration-t DMA group: K of tile t + 3 and V of tile t + 2; the two
+    // tile bases are looked up once per iteration
+    struct DmaGroup {
+        const uint16_t *k, *v;
+        CK_LDS char *kd, *vd;
+    };
+    auto dma_group = [&](int t) {
+        DmaGroup d;
+        d.k = a.k + tile_src(t + 3);
+        d.v = a.v + tile_src(t + 2);
+        d.kd = kring + ((t + 3) % kTSlots) * kTBytes + wid * kTBlk * 1024;
+        d.vd = vring + ((t + 2) % kTSlots) * kTBytes + wid * kTBlk * 1024;
+        return d;
+    };
+    auto dma_step = [&](const DmaGroup &d, int j) {
+        if (j < kTBlk) dma16(d.k + dma_off[j], d.kd + j * 1024);
+        else dma16(d.v + dma_off[j - kTBlk], d.vd + (j - kTBlk) * 1024);
+    };
+    auto zero_rows = [&](CK_LDS char *slot, int z0) {
+        for (int idx = tid; idx < (kTTok - z0) * 16; idx += kTW * 64) {
+            const int tt = z0 + (idx >> 4), c = idx & 15;
+            *reinterpret_cast<CK_LDS u32x4 *>(slot + tt * 256 + c * 16) = u32x4{0, 0, 0, 0};
+        }
+    };
+    auto page_ok = [&](int t) { return s_pages[t >> 1] >= 0; };
+
+    f32x16 oacc[RB][4];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) oacc[rb][db][i] = 0.f;
+    float m_run[RB], l_part[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        m_run[rb] = -INFINITY;
+        l_part[rb] = 0.f;
+    }
+
+    const int trG = (lane >> 4) & 3;
+    const int tr_row = (lane & 15) >> 2;
+    const int tr_e4 = lane & 3;
+    const int ktok = lane & 31;
+    auto vt_off = [&](int s16, int db, int second) {
+        const int t1 = 16 * s16 + 4 * (trG >> 1) + tr_row + 8 * second;
+        const int d = 32 * db + 16 * (trG & 1) + 4 * tr_e4;
+        return tile_off(t1, d >> 3) + (d & 7) * 2;
+    };
+    // K fragment f of a tile (f = 2 kk + q2: 16-dim step kk of token block q2)
+    auto kfrag = [&](const CK_LDS char *kb, int f) {
+        return *reinterpret_cast<const CK_LDS bf16x8 *>(kb + tile_off(32 * (f & 1) + ktok, 2 * (f >> 1) + hh));
+    };
+    // S^T of the tile in `kb` without interleaving (prologue)
+    auto qk_tile = [&](const CK_LDS char *kb, f32x16 (*sb)[2]) {
+        const f32x16 zero16 = {};
+#pragma unroll
+        for (int f = 0; f < 16; ++f) {
+            const bf16x8 kf = kfrag(kb, f);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+                sb[rb][f & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[rb][f >> 1],
+                                                                        f < 2 ? zero16 : sb[rb][f & 1], 0, 0, 0);
+        }
+    };
+
+    // ---- per-tile softmax pieces (p replaces s in place; P packed per 16 tokens) ----
+    // group s16 of row block rb: elements 8 (s16 & 1) .. + 8 of token block s16 / 2
+    float smax[RB], m_use[RB], dmv[RB], lsum[RB];
+    bool rescale = false;
+    auto soft_begin = [&]() {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            smax[rb] = -INFINITY;
+            lsum[rb] = 0.f;
+        }
+    };
+    auto max_chunk = [&](f32x16 (*sc)[2], int c) {  // c < 4 RB: 8 scores
+        const int rb = c >> 2, q2 = (c >> 1) & 1, e0 = 8 * (c & 1);
+#pragma unroll
+        for (int e = e0; e < e0 + 8; ++e) smax[rb] = fmaxf(smax[rb], sc[rb][q2][e]);
+    };
+    auto max_finish = [&]() {
+        bool any = false;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const float mx = max_xor32(smax[rb]) * a.scale_log2;
+            const float m_new = fmaxf(m_run[rb], mx);
+            m_use[rb] = (m_new == -INFINITY) ? 0.f : m_new;
+            dmv[rb] = exp2_fast(m_run[rb] - m_use[rb]);
+            m_run[rb] = m_new;
+            any |= dmv[rb] != 1.0f;
+        }
+        // O moves only when some row's max moved (wave-uniform)
+        rescale = __builtin_amdgcn_ballot_w64(any) != 0;
+    };
+    auto rescale_chunk = [&](int c) {  // c < 4 RB: 16 accumulators
+        if (rescale) {
+            const int rb = c >> 2, db = c & 3;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) oacc[rb][db][e] *= dmv[rb];
+        }
+    };
+    bf16x8 pbv[4][RB];
+    auto exp_chunk = [&](f32x16 (*sc)[2], int s16, int rb, int hf) {  // 4 scores; hf 1 packs the group
+        const int q2 = s16 >> 1, e0 = 8 * (s16 & 1) + 4 * hf;
+#pragma unroll
+        for (int e = e0; e < e0 + 4; ++e) {
+            const float pv = exp2_fast(fmaf(sc[rb][q2][e], a.scale_log2, -m_use[rb]));
+            sc[rb][q2][e] = pv;
+            lsum[rb] += pv;
+        }
+        if (hf == 1) pbv[s16][rb] = pack_p(sc[rb][q2], 8 * (s16 & 1));
+    };
+    auto soft_end = [&]() {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) l_part[rb] = l_part[rb] * dmv[rb] + lsum[rb];
+    };
+
+    // One full tile of the main loop (t + 1 < ntiles): a fixed issue order, one
+    // step per MFMA, fenced so the compiler keeps it.
+    //   QK of tile t + 1 (16 RB MFMAs, K fragments read four ahead) with tile t's
+    //   row max, step factors, O rescale and the exp of its 16-token groups 0-1;
+    //   PV of tile t (16 RB MFMAs, V^T fragments read two 4-fragment groups
+    //   ahead) with the exp of groups 2-3; a DMA every 4 RB MFMAs.
+    constexpr int kNQ = 16 * RB;
+    auto tile_body = [&](int t, f32x16 (*sc)[2], f32x16 (*sn)[2]) {
+        const CK_LDS char *kb = kring + ((t + 1) % kTSlots) * kTBytes;
+        const CK_LDS char *vb = vring + (t % kTSlots) * kTBytes;
+        const f32x16 zero16 = {};
+        const DmaGroup dg = dma_group(t);
+        soft_begin();
+        bf16x8 kfr[4];
+#pragma unroll
+        for (int f = 0; f < 4; ++f) kfr[f] = kfrag(kb, f);
+#pragma unroll
+        for (int i = 0; i < kNQ; ++i) {
+            const int f = i / RB, rb = i % RB;
+            sn[rb][f & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[f & 3], qf[rb][f >> 1],
+                                                                    f < 2 ? zero16 : sn[rb][f & 1], 0, 0, 0);
+            if (rb == RB - 1 && f + 4 < 16) kfr[f & 3] = kfrag(kb, f + 4);
+            // softmax slice: 4 RB max chunks, 4 RB rescale chunks, then the 4 RB exp
+            // chunks of groups 0-1 (2 RB per group: row block, half)
+            const int c = i;
+            if (c < 4 * RB) {
+                max_chunk(sc, c);
+                if (c == 4 * RB - 1) max_finish();
+            } else if (c < 8 * RB) {
+                rescale_chunk(c - 4 * RB);
+            } else if (c < 12 * RB) {
+                const int x = c - 8 * RB;
+                exp_chunk(sc, x / (2 * RB), (x / 2) % RB, x & 1);
+            }
+            if (i % (kNQ / (kTDma / 2)) == kNQ / (kTDma / 2) - 1) dma_step(dg, i / (kNQ / (kTDma / 2)));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        uint2 vlo[3][4], vhi[3][4];
+#pragma unroll
+        for (int s0 = 0; s0 < 2; ++s0)
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                vlo[s0][db] = lds_read_tr16(vb + vt_off(s0, db, 0));
+                vhi[s0][db] = lds_read_tr16(vb + vt_off(s0, db, 1));
+            }
+#pragma unroll
+        for (int i = 0; i < kNQ; ++i) {
+            const int fv = i / RB, rb = i % RB, s16 = fv >> 2, db = fv & 3, bsel = s16 % 3;
+            const bf16x8 vf = __builtin_bit_cast(
+                bf16x8, make_uint4(vlo[bsel][db].x, vlo[bsel][db].y, vhi[bsel][db].x, vhi[bsel][db].y));
+            oacc[rb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pbv[s16][rb], oacc[rb][db], 0, 0, 0);
+            if (rb == RB - 1 && s16 + 2 < 4) {
+                vlo[(s16 + 2) % 3][db] = lds_read_tr16(vb + vt_off(s16 + 2, db, 0));
+                vhi[(s16 + 2) % 3][db] = lds_read_tr16(vb + vt_off(s16 + 2, db, 1));
+            }
+            // exp of groups 2-3 (2 RB chunks each) over the first PV steps, each
+            // group finished before its first MFMA (group 2 at step 8 RB)
+            if (i < 4 * RB) exp_chunk(sc, 2 + i / (2 * RB), (i / 2) % RB, i & 1);
+            if (i % (kNQ / (kTDma / 2)) == kNQ / (kTDma / 2) - 1)
+                dma_step(dg, kTDma / 2 + i / (kNQ / (kTDma / 2)));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        soft_end();
+    };
+
+    f32x16 s_a[RB][2], s_b[RB][2];
+    // prologue: K of tiles 0-2 and V of tiles 0-1 in flight (repeats past the
+    // end). A split with no tokens (a request shorter than the split's start)
+    // issues nothing: every DMA source is a tile index clamped to ntiles - 1.
+    if (ntiles > 0) {
+#pragma unroll
+        for (int j = 0; j < kTBlk; ++j) {
+            dma_k(0, j);
+            dma_k(1, j);
+            dma_k(2, j);
+            dma_v(0, j);
+            dma_v(1, j);
+        }
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (ntiles > 0 && !page_ok(0)) {
+        zero_rows(kring, 0);
+        __syncthreads();
+    }
+    if (ntiles > 0 && wave_active) qk_tile(kring, s_a);
+
+    // every tile but the last is full (64 tokens)
+    auto tile_top = [&](int t) {
+        // this iteration reads K of tile t + 1 and V of tile t (issued two
+        // iterations ago); the previous iteration's group may stay in flight
+        wait_vmcnt<kTDma>();
+        __syncthreads();  // ... for every wave; and every wave is done with tile t - 1
+        const bool v_fill = !page_ok(t);
+        const bool k_fill = !page_ok(t + 1);
+        if (v_fill) zero_rows(vring + (t % kTSlots) * kTBytes, 0);
+        if (k_fill) zero_rows(kring + ((t + 1) % kTSlots) * kTBytes, 0);
+        if (v_fill || k_fill) __syncthreads();
+    };
+    auto idle_dmas = [&](int t) {
+        const DmaGroup dg = dma_group(t);
+#pragma unroll
+        for (int j = 0; j < kTDma; ++j) dma_step(dg, j);
+    };
+    int t = 0;
+    for (; t + 2 < ntiles; t += 2) {
+        tile_top(t);
+        if (wave_active) tile_body(t, s_a, s_b);
+        else idle_dmas(t);
+        tile_top(t + 1);
+        if (wave_active) tile_body(t + 1, s_b, s_a);
+        else idle_dmas(t + 1);
+    }
+    if (t + 1 < ntiles) {
+        tile_top(t);
+        if (wave_active) {
+            tile_body(t, s_a, s_b);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                s_a[rb][0] = s_b[rb][0];
+                s_a[rb][1] = s_b[rb][1];
+            }
+        } else {
+            idle_dmas(t);
+        }
+        ++t;
+    }
+    // the last tile: tokens past the split's end are masked (p = 0) and their V
+    // rows zeroed, so 0 * V cannot produce a NaN from rows nobody wrote
+    if (ntiles > 0) {
+        wait_vmcnt<0>();
+        __syncthreads();
+        const int nv = ntok - t * kTTok;
+        if (nv < kTTok || !page_ok(t)) {
+            zero_rows(vring + (t % kTSlots) * kTBytes, page_ok(t) ? nv : 0);
+            __syncthreads();
+        }
+        if (wave_active) {
+            if (nv < kTTok) {
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                    for (int q2 = 0; q2 < 2; ++q2)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) {
+                            const int tok = 32 * q2 + (e & 3) + 8 * (e >> 2) + 4 * hh;
+                            if (tok >= nv) s_a[rb][q2][e] = -INFINITY;
+                        }
+            }
+            const CK_LDS char *vb = vring + (t % kTSlots) * kTBytes;
+            soft_begin();
+            for (int c = 0; c < 4 * RB; ++c) max_chunk(s_a, c);
+            max_finish();
+            for (int c = 0; c < 4 * RB; ++c) rescale_chunk(c);
+#pragma unroll
+            for (int s16 = 0; s16 < 4; ++s16)
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) {
+                    exp_chunk(s_a, s16, rb, 0);
+                    exp_chunk(s_a, s16, rb, 1);
+                }
+            soft_end();
+#pragma unroll
+            for (int s16 = 0; s16 < 4; ++s16)
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    const uint2 lo = lds_read_tr16(vb + vt_off(s16, db, 0));
+                    const uint2 hi = lds_read_tr16(vb + vt_off(s16, db, 1));
+                    const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb)
+                        oacc[rb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pbv[s16][rb], oacc[rb][db], 0, 0, 0);
+                }
+        }
+    }
+
+    // ---- normalise and write whole rows --------------------------------------------
+    // Each wave writes its 32 RB rows through its own slab of the (now idle) rings
+    // (32 rows x 512 B = 16 KB per row block), re-laid out as whole 512-byte rows
+    // so each store instruction writes two contiguous rows.
+    float l_run[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) l_run[rb] = l_part[rb] + __shfl_xor(l_part[rb], 32);
+    __syncthreads();  // every wave is past its last ring read
+    if (!wave_active) return;  // wave-uniform
+    float *base = a.num_splits == 1 ? a.out : a.part_o + (int64_t)sp * a.num_rows * kD;
+    const int my_row = lane & 31;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const float inv = l_run[rb] > 0.f ? 1.0f / l_run[rb] : 0.f;
+        const float lse_v = l_run[rb] > 0.f ? (m_run[rb] + __log2f(l_run[rb])) * kLn2 : -INFINITY;
+        CK_LDS float *slab = (CK_LDS float *)smem + (wid * RB + rb) * (32 * kD);
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4) {
+                const f32x4 o = f32x4{oacc[rb][db][4 * c4 + 0] * inv, oacc[rb][db][4 * c4 + 1] * inv,
+                                      oacc[rb][db][4 * c4 + 2] * inv, oacc[rb][db][4 * c4 + 3] * inv};
+                const int chunk = (8 * db + 2 * c4 + hh) ^ my_row;
+                *reinterpret_cast<CK_LDS f32x4 *>(slab + my_row * kD + chunk * 4) = o;
+            }
+        if (row_valid[rb]) {
+            if (a.num_splits == 1) {
+                const float4 lv = make_float4(lse_v, lse_v, lse_v, lse_v);
+                *reinterpret_cast<float4 *>(a.lse + qrow[rb] * 8 + 4 * hh) = lv;
+            } else if (hh == 0) {
+                a.part_lse[(int64_t)sp * a.num_rows + qrow[rb]] = lse_v;
+            }
+        }
+        // the wave reads back only its own slab: the LDS ops of one wave complete in order
+        const int chunk = lane & 31;
+        const int rbase = wrow0 + rb * 32;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int rr = 2 * j + (lane >> 5);
+            const int64_t qr = __shfl((int)qrow[rb], rr);
+            const f32x4 o = *reinterpret_cast<const CK_LDS f32x4 *>(slab + rr * kD + ((chunk ^ rr) * 4));
+            if (rbase + rr < rows_b) *reinterpret_cast<f32x4 *>(base + qr * kD + chunk * 4) = o;
+        }
+    }
+}
+
+// 256-row variant for requests whose rows of one kv head fill more than 128:
+// 8 waves (two per SIMD), wave w owns query rows 32 w .. + 32 and every token
+// of them. Each 64-token K/V tile in LDS feeds 256 rows (twice the MFMA work
+// per DMA byte and per barrier of the 128-row kernel), and while one wave of a
+// SIMD waits on a fragment read, a DMA issue or its softmax, the other issues
+// MFMAs. Per tile: QK (16 MFMAs, K fragments read four ahead), softmax with
+// the running max moved once per tile, PV (16 MFMAs, V^T fragments read one
+// 16-token group ahead). A 4-slot ring of K+V tiles, three tiles of DMA lead.
+constexpr int kWW = 8;
+constexpr int kWRows = kWW * 32;
+constexpr int kWSlots = 4;
+constexpr int kWStage = 2 * kTBytes;               // K + V of one tile (32 KB)
+constexpr int kWBlk = kTBytes / 1024 / kWW;        // 1-KB DMAs of K (and of V) per wave per tile (2)
+constexpr int kWLds = kWSlots * kWStage + kMaxSplitPages * 4;
+
+__global__ __launch_bounds__(kWW * 64) void stage1_wide_kernel(Stage1Args a) {
+    extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+    CK_LDS char *smem = (CK_LDS char *)smem_raw;
+    CK_LDS int *s_pages = (CK_LDS int *)(smem + kWSlots * kWStage);
+
+    const int tid = threadIdx.x;
+    const int wid = tid >> 6;
+    const int lane = tid & 63;
+    const int hh = lane >> 5;
+
+    uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
+    const int mt = w % a.mtiles;
+    w /= a.mtiles;
+    const int sp = w % a.num_splits;
+    w /= a.num_splits;
+    const int g = w % a.kv_heads;
+    const int b = w / a.kv_heads;
+
+    int qlen, qs;
+    if (a.q_len_uniform > 0) {
+        qlen = a.q_len_uniform;
+        qs = b * qlen;
+    } else {
+        qlen = (int)a.q_seqlens[b];
+        qs = a.q_start[b];
+    }
+    const int rows_b = qlen * a.group;
+    const int row0 = mt * kWRows;
+    if (row0 >= rows_b) return;  // uniform over the workgroup
+
+    const int wrow0 = row0 + wid * 32;
     const bool wave_active = wrow0 < rows_b;
     const int r = wrow0 + (lane & 31);
     const bool row_valid = r < rows_b;
     const int t_local = r / a.group;
     const int h = g * a.group + (r - t_local * a.group);
     const int64_t qrow = (int64_t)(qs + t_local) * a.num_heads + h;
-
-    // Q as the B operand of S^T = K Q^T: lane holds dims 16kk + 8hh .. +8.
     bf16x8 qf[8];
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
@@ -164,15 +638,12 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
             qf[kk] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
         }
     }
-    // Page ids are read for the split's whole page range inside the table row,
-    // whatever the kv length (only those below it are used), so they, Q and the
-    // kv length are fetched together in one round trip.
-    const int kv_lo = sp * a.split_len;  // a multiple of kPage
+    const int kv_lo = sp * a.split_len;
     {
         const int pg0 = kv_lo / kPage;
         const int64_t avail = a.bt_cols - pg0;
         const int pg_n = (int)min((int64_t)(a.split_len / kPage), avail > 0 ? avail : (int64_t)0);
-        for (int pi = tid; pi < pg_n; pi += kThreads) {
+        for (int pi = tid; pi < pg_n; pi += kWW * 64) {
             const int page = a.bt[(int64_t)b * a.bt_cols + pg0 + pi];
             s_pages[pi] = (page >= 0 && (int64_t)page < a.num_blocks) ? page : -1;
         }
@@ -181,236 +652,175 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
     const int64_t kv_lim = a.bt_cols * kPage;
     if (kvl > kv_lim) kvl = kv_lim;
     if (kvl > a.kv_cap) kvl = a.kv_cap;
-    if (kvl < 0 || a.num_blocks <= 0) kvl = 0;  // no pool: nothing to attend to
+    if (kvl < 0 || a.num_blocks <= 0) kvl = 0;
     int kv_hi = kv_lo + a.split_len;
     if (kv_hi > (int)kvl) kv_hi = (int)kvl;
-    const int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + kTileN - 1) / kTileN : 0;
+    const int ntok = kv_hi > kv_lo ? kv_hi - kv_lo : 0;
+    const int ntiles = (ntok + kTTok - 1) / kTTok;
 
-    // Q and page ids must be resident before the DMA ring starts: the compiler
-    // does not count the inline-asm DMAs, so a wait it deferred into the loop
-    // would also drain every tile in flight.
     wait_vmcnt<0>();
     __syncthreads();  // s_pages visible
 
     const int64_t head_stride = (int64_t)a.kv_heads * kD;
-    // DMA lane geometry: one wave instruction moves 4 token rows (1 KB); lane ->
-    // token 4*blk + lane/16 and LDS chunk lane%16, which holds global chunk
-    // (lane%16) ^ tile_swz(token).
-    const int dma_tt = lane >> 4;
-    const int dma_pc = lane & 15;
-
-    auto issue_tile = [&](int i) {
-        const int j0 = kv_lo + i * kTileN;
-        // an invalid page is zero-filled at wait time; its DMAs still go out (from
-        // page 0) so every wave keeps exactly kDmaPerTile operations per tile and
-        // the vmcnt-based waits stay exact
-        const int raw_page = s_pages[(j0 - kv_lo) / kPage];
-        const int page = raw_page < 0 ? 0 : raw_page;
-        CK_LDS char *kb = smem + (i % kStages) * kStageBytes;
-        CK_LDS char *vb = kb + kTileBytes;
-        const int64_t tok0 = (int64_t)page * kPage + (j0 % kPage);
+    uint32_t dma_off[kWBlk];
 #pragma unroll
-        for (int j = 0; j < kDmaPerTile / 2; ++j) {
-            const int blk = wid * (kDmaPerTile / 2) + j;
-            const int tt = blk * 4 + dma_tt;
-            const int c = dma_pc ^ tile_swz(tt);
-            const int64_t off = (tok0 + tt) * head_stride + g * kD + c * 8;
-            dma16(a.k + off, kb + blk * 1024);
-            dma16(a.v + off, vb + blk * 1024);
+    for (int j = 0; j < kWBlk; ++j) {
+        const int tt = (wid * kWBlk + j) * 4 + (lane >> 4);
+        dma_off[j] = (uint32_t)(tt * head_stride + g * kD + (((lane & 15) ^ tile_swz(tt)) << 3));
+    }
+    // DMAs of tile t (t < ntiles) into ring slot t % 4
+    auto issue = [&](int t) {
+        const int raw = __builtin_amdgcn_readfirstlane(s_pages[t >> 1]);
+        const int64_t base = ((int64_t)(raw < 0 ? 0 : raw) * kPage + (t & 1) * kTTok) * head_stride;
+        CK_LDS char *kd = smem + (t % kWSlots) * kWStage + wid * kWBlk * 1024;
+#pragma unroll
+        for (int j = 0; j < kWBlk; ++j) {
+            dma16(a.k + base + dma_off[j], kd + j * 1024);
+            dma16(a.v + base + dma_off[j], kd + kTBytes + j * 1024);
         }
     };
 
-    // ---- online softmax state (one query row per lane, halves agree) ---------------
     f32x16 oacc[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[db][i] = 0.f;
     float m_run = -INFINITY;
-    float l_part = 0.f;  // row sum over the tokens of this lane half
+    float l_part = 0.f;
 
-    // Tiles go in pairs: one barrier, one max update and at most one O rescale
-    // per 128 kv tokens (64 per wave). Pair p (tiles 2p, 2p + 1) is computed
-    // while pair p + 1 lands; the ring's four slots hold exactly those two pairs.
-    static_assert(kStages == 4, "two pairs of tiles in the ring");
-    for (int i = 0; i < 2 && i < ntiles; ++i) issue_tile(i);
-
-    // per-lane LDS offsets (loop invariant): K fragment rows of this token half,
-    // and the V^T transpose-read addresses. Transpose reads: lane group
-    // G = lane/16 covers dims 16*(G%2) + 0..15 of each 32-dim block and the
-    // token quad 4*(G/2); its source lane s addresses token s/4, dims 4*(s%4)..+3.
-    const int ktok = th * 32 + (lane & 31);
     const int trG = (lane >> 4) & 3;
     const int tr_row = (lane & 15) >> 2;
     const int tr_e4 = lane & 3;
-
-    // S^T for this wave's token half of the tile in `slot`; tokens past nvalid -> -inf
-    auto qk_tile = [&](int slot, int nvalid, f32x16 &sacc) {
-        const CK_LDS char *kb = smem + slot * kStageBytes;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-            const bf16x8 kf = *reinterpret_cast<const CK_LDS bf16x8 *>(kb + tile_off(ktok, 2 * kk + hh));
-            sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sacc, 0, 0, 0);
-        }
-        if (nvalid < kTileN) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int tok = th * 32 + (e & 3) + 8 * (e >> 2) + 4 * hh;
-                if (tok >= nvalid) sacc[e] = -INFINITY;
-            }
-        }
-    };
-    // O^T += V^T P^T over this half's 2 k-steps of 16 tokens of the tile in `slot`
-    auto pv_tile = [&](int slot, const f32x16 &pacc) {
-        const CK_LDS char *vb = smem + slot * kStageBytes + kTileBytes;
-#pragma unroll
-        for (int ss = 0; ss < 2; ++ss) {
-            const int s = 2 * th + ss;
-            const bf16x8 pb = pack_p(pacc, ss * 8);
-            const int t1 = 16 * s + 4 * (trG >> 1) + tr_row;  // first read; second is t1 + 8
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const int d = 32 * db + 16 * (trG & 1) + 4 * tr_e4;  // 4 dims this lane addresses
-                const int c = d >> 3, half = (d & 7) * 2;
-                const uint2 lo = lds_read_tr16(vb + tile_off(t1, c) + half);
-                const uint2 hi = lds_read_tr16(vb + tile_off(t1 + 8, c) + half);
-                const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-                oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb, oacc[db], 0, 0, 0);
-            }
-        }
+    const int ktok = lane & 31;
+    auto vt_off = [&](int s16, int db, int second) {
+        const int t1 = 16 * s16 + 4 * (trG >> 1) + tr_row + 8 * second;
+        const int d = 32 * db + 16 * (trG & 1) + 4 * tr_e4;
+        return tile_off(t1, d >> 3) + (d & 7) * 2;
     };
 
-    for (int i = 0; i < ntiles; i += 2) {
-        const bool two = i + 1 < ntiles;
-        // this pair was issued one pair ago and nothing after it: all landed
-        wait_vmcnt<0>();
-        __syncthreads();
-        int nv[2];
-        bool fill = false;
+    for (int t = 0; t < 3 && t < ntiles; ++t) issue(t);
+    for (int t = 0; t < ntiles; ++t) {
+        // tile t has landed once at most the DMAs of the tiles after it remain
+        const int after = min(2, ntiles - 1 - t);
+        if (after >= 2) wait_vmcnt<4 * kWBlk>();
+        else if (after == 1) wait_vmcnt<2 * kWBlk>();
+        else wait_vmcnt<0>();
+        __syncthreads();  // ... in every wave; every wave is done with tile t - 1
+        const int nv = min(kTTok, ntok - t * kTTok);
+        const bool ok = s_pages[t >> 1] >= 0;
+        CK_LDS char *kb = smem + (t % kWSlots) * kWStage;
+        CK_LDS char *vb = kb + kTBytes;
+        if (nv < kTTok || !ok) {
+            // rows past the split's end or of an invalid page: zero them so 0 * V
+            // cannot produce a NaN (an invalid page reads as zero rows)
+            const int z0 = ok ? nv : 0;
+            for (int idx = tid; idx < (kTTok - z0) * 16; idx += kWW * 64) {
+                const int tt = z0 + (idx >> 4), c = idx & 15;
+                *reinterpret_cast<CK_LDS u32x4 *>(kb + tt * 256 + c * 16) = u32x4{0, 0, 0, 0};
+                *reinterpret_cast<CK_LDS u32x4 *>(vb + tt * 256 + c * 16) = u32x4{0, 0, 0, 0};
+            }
+            __syncthreads();
+        }
+        if (t + 3 < ntiles) issue(t + 3);  // into the slot of tile t - 1
+        if (!wave_active) continue;
+
+        // S^T of the two 32-token blocks, K fragments read four ahead
+        f32x16 sb[2];
+        {
+            const f32x16 zero16 = {};
+            auto kfrag = [&](int f) {
+                return *reinterpret_cast<const CK_LDS bf16x8 *>(kb + tile_off(32 * (f & 1) + ktok, 2 * (f >> 1) + hh));
+            };
+            bf16x8 kfr[4];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            nv[t] = 0;
-            if (t == 1 && !two) continue;
-            const int j0 = kv_lo + (i + t) * kTileN;
-            nv[t] = min(kTileN, kv_hi - j0);
-            const bool page_ok = s_pages[(j0 - kv_lo) / kPage] >= 0;
-            if (nv[t] < kTileN || !page_ok) {
-                // rows past the sequence end (or of an invalid page) may hold
-                // anything: zero them so 0 * V cannot produce a NaN
-                CK_LDS char *kb = smem + ((i + t) % kStages) * kStageBytes;
-                CK_LDS char *vb = kb + kTileBytes;
-                const int z0 = page_ok ? nv[t] : 0;
-                for (int idx = tid; idx < (kTileN - z0) * 16; idx += kThreads) {
-                    const int tt = z0 + (idx >> 4), c = idx & 15;
-                    *reinterpret_cast<CK_LDS u32x4 *>(kb + tt * 256 + c * 16) = u32x4{0, 0, 0, 0};
-                    *reinterpret_cast<CK_LDS u32x4 *>(vb + tt * 256 + c * 16) = u32x4{0, 0, 0, 0};
-                }
-                fill = true;
+            for (int f = 0; f < 4; ++f) kfr[f] = kfrag(f);
+#pragma unroll
+            for (int f = 0; f < 16; ++f) {
+                sb[f & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[f & 3], qf[f >> 1], f < 2 ? zero16 : sb[f & 1],
+                                                                    0, 0, 0);
+                if (f + 4 < 16) kfr[f & 3] = kfrag(f + 4);
             }
         }
-        if (fill) __syncthreads();
-        // the previous pair's slots are free: the pair after this one goes there
+        if (nv < kTTok) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-            if (i + 2 + t < ntiles) issue_tile(i + 2 + t);
-
-        const bool act0 = wave_active && th * 32 < nv[0];
-        const bool act1 = wave_active && th * 32 < nv[1];  // tile i + 1 exists only after a full tile i
-        if (act0) {
-            f32x16 s0, s1;
-            qk_tile(i % kStages, nv[0], s0);
-            if (act1) qk_tile((i + 1) % kStages, nv[1], s1);
-            // row max of the unscaled scores over both tiles; the scale is > 0,
-            // so scaling the max gives the max of the scaled scores
-            float smax = -INFINITY;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) smax = fmaxf(smax, s0[e]);
-            if (act1) {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) smax = fmaxf(smax, s1[e]);
-            }
-            smax = max_xor32(smax) * a.scale_log2;  // the row's other tokens sit in lane l ^ 32
-            const float m_new = fmaxf(m_run, smax);
-            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-            const float dm = exp2_fast(m_run - m_use);
-            // p = exp2(s * scale * log2(e) - m): one FMA and one exp2 per score
-            float ls = 0.f;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float p = exp2_fast(fmaf(s0[e], a.scale_log2, -m_use));
-                s0[e] = p;
-                ls += p;
-            }
-            if (act1) {
+            for (int q2 = 0; q2 < 2; ++q2)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const float p = exp2_fast(fmaf(s1[e], a.scale_log2, -m_use));
-                    s1[e] = p;
-                    ls += p;
+                    const int tok = 32 * q2 + (e & 3) + 8 * (e >> 2) + 4 * hh;
+                    if (tok >= nv) sb[q2][e] = -INFINITY;
+                }
+        }
+        float smax = -INFINITY;
+#pragma unroll
+        for (int q2 = 0; q2 < 2; ++q2)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) smax = fmaxf(smax, sb[q2][e]);
+        smax = max_xor32(smax) * a.scale_log2;
+        const float m_new = fmaxf(m_run, smax);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        const float dm = exp2_fast(m_run - m_use);
+        m_run = m_new;
+        float ls = 0.f;
+        bf16x8 pb[4];
+#pragma unroll
+        for (int q2 = 0; q2 < 2; ++q2) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float pv = exp2_fast(fmaf(sb[q2][e], a.scale_log2, -m_use));
+                sb[q2][e] = pv;
+                ls += pv;
+            }
+            pb[2 * q2] = pack_p(sb[q2], 0);
+            pb[2 * q2 + 1] = pack_p(sb[q2], 8);
+        }
+        l_part = l_part * dm + ls;
+        if (__builtin_amdgcn_ballot_w64(dm != 1.0f)) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) oacc[db][e] *= dm;
+        }
+        // O^T += V^T P^T, V^T fragments read one 16-token group ahead
+        {
+            uint2 vlo[2][4], vhi[2][4];
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                vlo[0][db] = lds_read_tr16(vb + vt_off(0, db, 0));
+                vhi[0][db] = lds_read_tr16(vb + vt_off(0, db, 1));
+            }
+#pragma unroll
+            for (int s16 = 0; s16 < 4; ++s16) {
+                if (s16 + 1 < 4) {
+#pragma unroll
+                    for (int db = 0; db < 4; ++db) {
+                        vlo[(s16 + 1) & 1][db] = lds_read_tr16(vb + vt_off(s16 + 1, db, 0));
+                        vhi[(s16 + 1) & 1][db] = lds_read_tr16(vb + vt_off(s16 + 1, db, 1));
+                    }
+                }
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    const uint2 lo = vlo[s16 & 1][db], hi = vhi[s16 & 1][db];
+                    const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[s16], oacc[db], 0, 0, 0);
                 }
             }
-            // the two lane halves hold different tokens of the row: their sums
-            // are kept apart and added once after the loop
-            l_part = l_part * dm + ls;
-            m_run = m_new;
-            // rescale only when some row's max moved (wave-uniform branch)
-            if (__builtin_amdgcn_ballot_w64(dm != 1.0f)) {
-#pragma unroll
-                for (int db = 0; db < 4; ++db)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) oacc[db][e] *= dm;
-            }
-            pv_tile(i % kStages, s0);
-            if (act1) pv_tile((i + 1) % kStages, s1);
         }
     }
 
-    // ---- merge the two token halves, then write whole rows --------------------------
-    // The ring is free now. Wave (rb, 1) parks its O^T accumulators in the
-    // 16 KB slab of row block rb; wave (rb, 0) folds them into its own, then
-    // rewrites the slab as 32 normalised fp32 rows of 512 B (16-byte chunks
-    // XOR-swizzled by row) and stores two whole rows per instruction, so every
-    // global store is a full, contiguous 1 KB.
+    // ---- normalise and write whole rows through the idle ring ------------------------
     const float l_run = l_part + __shfl_xor(l_part, 32);
-    __syncthreads();
-    CK_LDS float *slab = (CK_LDS float *)smem + rb * (32 * kD);  // [16 quads][64 lanes][4]
-    CK_LDS float *xm = (CK_LDS float *)smem + 4 * 32 * kD;  // past the four slabs
-    CK_LDS float *xl = xm + 4 * 64;
-    if (th == 1) {
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int c4 = 0; c4 < 4; ++c4)
-                *reinterpret_cast<CK_LDS f32x4 *>(slab + ((db * 4 + c4) * 64 + lane) * 4) =
-                    f32x4{oacc[db][4 * c4], oacc[db][4 * c4 + 1], oacc[db][4 * c4 + 2], oacc[db][4 * c4 + 3]};
-        xm[rb * 64 + lane] = m_run;
-        xl[rb * 64 + lane] = l_run;
-    }
-    __syncthreads();
-    if (th == 1 || !wave_active) return;  // wave-uniform
-    const float m1 = xm[rb * 64 + lane], l1 = xl[rb * 64 + lane];
-    const float mn = fmaxf(m_run, m1);
-    const float mu = mn == -INFINITY ? 0.f : mn;
-    const float f0 = exp2_fast(m_run - mu), f1 = exp2_fast(m1 - mu);
-    const float lt = l_run * f0 + l1 * f1;
-    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-    const float lse_v = lt > 0.f ? (mn + __log2f(lt)) * kLn2 : -INFINITY;
-    f32x4 o1[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q) o1[q] = *reinterpret_cast<const CK_LDS f32x4 *>(slab + (q * 64 + lane) * 4);
-    // lane holds row lane%32, dims 32*db + 8*c4 + 4*hh .. +3 = 16-byte chunk 8*db + 2*c4 + hh
+    __syncthreads();  // every wave is past its last ring read
+    if (!wave_active) return;  // wave-uniform
+    const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+    const float lse_v = l_run > 0.f ? (m_run + __log2f(l_run)) * kLn2 : -INFINITY;
+    CK_LDS float *slab = (CK_LDS float *)smem + wid * (32 * kD);
     const int my_row = lane & 31;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int c4 = 0; c4 < 4; ++c4) {
-            const int q = db * 4 + c4;
-            const f32x4 o = f32x4{(oacc[db][4 * c4 + 0] * f0 + o1[q][0] * f1) * inv,
-                                  (oacc[db][4 * c4 + 1] * f0 + o1[q][1] * f1) * inv,
-                                  (oacc[db][4 * c4 + 2] * f0 + o1[q][2] * f1) * inv,
-                                  (oacc[db][4 * c4 + 3] * f0 + o1[q][3] * f1) * inv};
+            const f32x4 o = f32x4{oacc[db][4 * c4 + 0] * inv, oacc[db][4 * c4 + 1] * inv,
+                                  oacc[db][4 * c4 + 2] * inv, oacc[db][4 * c4 + 3] * inv};
             const int chunk = (8 * db + 2 * c4 + hh) ^ my_row;
             *reinterpret_cast<CK_LDS f32x4 *>(slab + my_row * kD + chunk * 4) = o;
         }
@@ -422,12 +832,11 @@ __global__ __launch_bounds__(kThreads) void stage1_kernel(Stage1Args a) {
             a.part_lse[(int64_t)sp * a.num_rows + qrow] = lse_v;
         }
     }
-    // the wave reads back only its own slab: no barrier, the LDS ops of one wave complete in order
     float *base = a.num_splits == 1 ? a.out : a.part_o + (int64_t)sp * a.num_rows * kD;
     const int chunk = lane & 31;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-        const int rr = 2 * j + (lane >> 5);  // row within the block
+        const int rr = 2 * j + (lane >> 5);
         const int64_t qr = __shfl((int)qrow, rr);
         const f32x4 o = *reinterpret_cast<const CK_LDS f32x4 *>(slab + rr * kD + ((chunk ^ rr) * 4));
         if (wrow0 + rr < rows_b) *reinterpret_cast<f32x4 *>(base + qr * kD + chunk * 4) = o;
@@ -485,13 +894,19 @@ __global__ __launch_bounds__(256) void stage1_combine_kernel(const float *part_o
 int64_t ceil_div(int64_t x, int64_t y) { return (x + y - 1) / y; }
 
 struct Plan {
-    int64_t mtiles, splits, split_len, ws_bytes;
+    int64_t roww, mtiles, splits, split_len, ws_bytes;
 };
 
 int make_plan(int64_t batch, int64_t max_q_len, int64_t num_heads, int64_t kv_heads, int64_t kv_cap,
               int64_t forced_splits, Plan *p) {
     const int64_t group = num_heads / kv_heads;
-    p->mtiles = ceil_div(max_q_len * group, kRows);
+    // 256-row workgroups (8 waves) once a request's rows for one kv head fill
+    // more than 128 and the 256-row grid still holds at least one workgroup per
+    // CU with >= 1024 tokens per split; 128-row workgroups (4 waves) otherwise
+    const int64_t rows = max_q_len * group;
+    p->roww = 1;
+    if (rows > 128 && batch * kv_heads * ceil_div(rows, 256) * ceil_div(kv_cap, 1024) >= 256) p->roww = 2;
+    p->mtiles = ceil_div(rows, 128 * p->roww);
     const int64_t base = batch * kv_heads * p->mtiles;
     int64_t s = forced_splits;
     if (s <= 0) {
@@ -603,10 +1018,17 @@ int ck::stage1_launch(const void *q, const void *k, const void *v, const int32_t
 
     const int64_t grid = batch * kv_heads * p.mtiles * p.splits;
     if (grid <= 0 || grid > 0x7FFFFFFF) return CK_E_INVALID_ARG;
-    static std::atomic<uint64_t> lds_set{0};
-    rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&stage1_kernel), kLdsBytes, lds_set);
-    if (rc != CK_OK) return rc;
-    hipLaunchKernelGGL(stage1_kernel, dim3((unsigned)grid), dim3(kThreads), kLdsBytes, s, a);
+    if (p.roww == 2) {
+        static std::atomic<uint64_t> lds_set_w{0};
+        rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&stage1_wide_kernel), kWLds, lds_set_w);
+        if (rc != CK_OK) return rc;
+        hipLaunchKernelGGL(stage1_wide_kernel, dim3((unsigned)grid), dim3(kWW * 64), kWLds, s, a);
+    } else {
+        static std::atomic<uint64_t> lds_set1{0};
+        rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&stage1_tile_kernel<1>), kTLds, lds_set1);
+        if (rc != CK_OK) return rc;
+        hipLaunchKernelGGL(stage1_tile_kernel<1>, dim3((unsigned)grid), dim3(kTW * 64), kTLds, s, a);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
     if (p.splits > 1 && combine) {
