@@ -60,19 +60,18 @@ def test_stage1_plan_and_validation():
 def test_suffix_plan_and_validation():
     s, w = abi.suffix_plan(64, 32, 8, 128, 4096)
     assert s >= 1 and (w == 0) == (s == 1)
-    # the grid holds the workgroups that can be resident at once: two per CU
-    # (256 CUs) up to 5 heads per kv head, one per CU above (more VGPRs)
-    assert abi.suffix_plan(64, 32, 8, 128, 4096)[0] == 2 * 256 // 8
-    assert abi.suffix_plan(64, 40, 8, 128, 4096)[0] == 2 * 256 // 8
-    assert abi.suffix_plan(64, 64, 8, 128, 4096)[0] == 256 // 8
-    assert abi.suffix_plan(64, 8, 1, 128, 4096)[0] == 256
+    # the grid holds 512 workgroups (two per CU on 256 CUs) over all kv head groups
+    assert abi.suffix_plan(64, 32, 8, 128, 4096)[0] == 512 // 8
+    assert abi.suffix_plan(64, 40, 8, 128, 4096)[0] == 512 // 8
+    assert abi.suffix_plan(64, 64, 8, 128, 4096)[0] == 512 // 8
+    assert abi.suffix_plan(64, 8, 1, 128, 4096)[0] == 512
     L = abi.lib()
     out = ctypes.c_int64(0)
-    # 16 query heads per kv head: two kv head groups of 8, one workgroup per CU
-    assert abi.suffix_plan(4, 64, 4, 128, 128)[0] == 256 // 8
-    # 12 per kv head: two groups of 6; 11 (prime): eleven groups of 1, two workgroups per CU
-    assert abi.suffix_plan(4, 48, 4, 128, 128)[0] == 256 // 8
-    assert abi.suffix_plan(4, 11, 1, 128, 128)[0] == 2 * 256 // 11
+    # 16 query heads per kv head: two kv head groups of 8 per kv head
+    assert abi.suffix_plan(4, 64, 4, 128, 128)[0] == 512 // 8
+    # 12 per kv head: two groups of 6; 11 (prime): eleven groups of 1
+    assert abi.suffix_plan(4, 48, 4, 128, 128)[0] == 512 // 8
+    assert abi.suffix_plan(4, 11, 1, 128, 128)[0] == 512 // 11
     p = ctypes.c_void_p(16)
     assert L.ck_suffix_decode(p, p, p, p, 1, p, 0, 8, 8, 128, 1, 128, 0, 0.1, 128, 1, p, p, None, 0, None) == 0
     assert L.ck_suffix_decode(p, p, p, p, 1, p, 4, 8, 8, 128, 1, 128, 2, 0.1, 128, 1, p, p, p, 1 << 20, None) == -1

@@ -11,75 +11,128 @@
 // fp32 P and fp32 accumulation (no bf16 rounding of P: there is no matrix
 // core here to feed), O = acc / l, LSE = ln(l) + max.
 //
-// MI355X design: memory-bound streaming with a persistent, balanced grid.
-// * Suffix lengths vary widely (geometric in the benchmark), and a workgroup
-//   pays several microseconds of start-up (lengths, page ids, first DMA round
-//   trip) before its first byte of K/V. So the work is cut into windows of 64
-//   tokens of one sequence (the last window of a sequence may be short), and
-//   workgroup (kv head g, chunk c) takes the c-th 1/P of the list of all
-//   windows, crossing sequence boundaries: every workgroup streams the same
-//   number of windows and starts once. Window and length prefix sums are built
-//   per workgroup in LDS from the device-side lengths.
+// MI355X design: HBM-bound streaming with a persistent, balanced grid, and as
+// little vector-ALU work per byte as the arithmetic allows (a wave64 vector
+// instruction occupies its SIMD for 4 cycles; at 8 TB/s a CU receives about
+// 15 bytes per cycle, so every instruction per K/V byte counts).
+// * Suffix lengths vary widely (geometric in the benchmark), so the work is cut
+//   into windows of 64 tokens of one sequence (the last window of a sequence
+//   may be short), and workgroup (kv head group g, chunk c) takes the c-th 1/P
+//   of the list of all windows, crossing sequence boundaries: every workgroup
+//   streams the same number of windows and starts once. Two workgroups per CU.
+// * Start-up: lengths -> window prefix sums (block scan in LDS), then a table
+//   of the workgroup's windows (page id, first token, valid tokens, sequence,
+//   segment start/end) built in parallel in one round trip that also copies
+//   the first q rows into LDS. The streaming loop reads the table from LDS; no
+//   load in the loop depends on another load.
 // * Two paged K/V layouts: NHD [blocks, 128, kv_heads, 128] (the stage-1 pool)
 //   and BNSD [blocks, kv_heads, 128, 128] (the layout the reference's stage-2
 //   op reads, ascend-kernel/README.md:182-183), so a BNSD pool needs no
-//   transposing copy. A page, a token and a kv head are three strides; each
-//   DMA moves four 256-byte token rows of one kv head either way.
-// * K and V rows stream through a 2-stage LDS ring (one window, 32 KB, per
-//   stage) by global->LDS DMA, continuously across sequence boundaries. The
-//   ring, prefix sums and scratch take about 78 KB, so two workgroups share a
-//   CU (16 waves): while one waits on its stage the other computes, which
-//   hides more latency than a deeper ring in one workgroup per CU. A stage's
-//   DMA group also carries a block-table entry kStages - 1 windows ahead (so
-//   page ids never wait on memory inside the loop) and, on the first window of
-//   a sequence, its q rows. Each wave counts its own vector-memory
-//   operations (DMAs and output stores) and waits for exactly one stage. Half
-//   the waves issue the next group right after the stage barrier and half after
-//   their compute, so the DMA issue of one half overlaps the other's arithmetic.
-// * Scores: lane (t, c) of wave w holds token 8w + t, dims 8c..8c+7 and
-//   64+8c..64+8c+7; q.k is eight packed bf16 dot products (v_dot2_f32_bf16,
-//   two chains) and a 3-step DPP sum over the token's 8 lanes.
-// * Softmax: the running max is uniform over the wave and moves only when a
-//   score exceeds it by more than 2^kTau (a wave-uniform branch), so rescaling
-//   is rare; any reference point gives the same O and LSE.
-// * Values: lane l accumulates dims 2l, 2l+1 of every query head over all of
-//   the wave's tokens; the token weights reach the lanes as LDS broadcasts.
-//   Closing a sequence therefore needs only a cross-wave merge through the
-//   just-consumed ring stage.
+//   transposing copy. A page, a token and a kv head are three strides.
+// * K and V go straight from HBM into registers by buffer loads: no LDS
+//   staging and no barrier in the streaming loop. Each window gets a buffer
+//   descriptor (its first row as base, its 64 rows as range) built with scalar
+//   instructions, so a lane's address is a fixed offset; lanes whose tokens lie
+//   past the sequence's end use an out-of-range offset, which returns zeros and
+//   moves no bytes, and an invalid page id gets an empty range: its rows read
+//   as zeros, the semantics of the pool's unmapped pages.
+// * Each wave owns 8 tokens of every window. For K, lane (t, c) holds token t
+//   and dims 8c .. 8c+7 and 64+8c .. 64+8c+7 (two 16-byte loads); for V, lane
+//   (hf, d) holds dims 4d .. 4d+3 of tokens hf, 2 + hf, 4 + hf, 6 + hf (four
+//   8-byte loads), so the value accumulators are only 4 per query head. A wave
+//   issues the loads of its next window before computing the current one (a
+//   two-slot register ring), so the memory pipe never waits on arithmetic or
+//   on another wave.
+// * Scores: 8 packed bf16 dot products (v_dot2_f32_bf16) and a 3-step DPP sum
+//   over the 8 lanes of a token. The running max is uniform over the wave and
+//   moves only when a score exceeds it by more than 2^kTau (a wave-uniform
+//   branch), so rescaling is rare; any reference point gives the same O and LSE.
+// * Values: p of the wave's 8 tokens goes through a 32-float LDS row per wave
+//   (one write, four broadcast reads), then 4 FMAs per token and head.
+// * Closing a sequence never stops the stream: each wave folds its two
+//   half-waves with one lane swap per accumulator, writes its partial (O, m, l)
+//   into the segment's slot of an LDS exchange ring and counts itself in with an
+//   LDS atomic; the last of the 8 waves merges the 8 partials and writes the
+//   result while the others go on. A wave waits for a ring slot only if it runs
+//   a whole ring ahead of the slowest wave, which itself never waits, so every
+//   wait ends.
+// * The range is processed in phases of at most 512 windows and 8 segments.
+//   A phase starts with one round trip that fills the window table and copies
+//   the q rows of its segments into LDS (read per window, which costs far less
+//   LDS bandwidth than the registers it frees); the phase's loop has no barrier.
 // * A segment that is a whole sequence writes bf16 O and the LSE directly; a
 //   sequence cut by a chunk boundary leaves fp32 partials that a small fix-up
 //   kernel folds (it also writes O = 0, LSE = -inf for empty suffixes).
+#include <type_traits>
+
 #include "ck_common.h"
 #include "ck_internal.h"
 
 namespace ck {
 namespace {
 
+// Calls f(std::integral_constant<int, I>{}) for I = 0 .. N - 1 (unrolled, I usable
+// as a compile-time index).
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for_from(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for_from<I + 1, N>(f);
+    }
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_from<0, N>(f);
+}
+
 constexpr int kD = 128;
 constexpr int kPage = 128;
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
-constexpr int kWin = 64;                           // tokens per window (= per ring stage)
-constexpr int kStages = 2;
-constexpr int kTileBytes = kWin * kD * 2;          // 16 KB of K (and of V) per stage
+constexpr int kWin = 64;            // tokens per window: 8 per wave
 constexpr int kMaxGroup = 8;
-constexpr int kQBytes = kMaxGroup * kD * 2;        // q rows of one (sequence, kv head)
-constexpr int kStageBytes = 2 * kTileBytes + kQBytes;
-constexpr int kMaxBatch = 1024;                    // sequences per launch (prefix sums in LDS)
-constexpr int kBlocksPerCu = 2;                    // resident workgroups per CU the grid is sized for
-constexpr int kPgRing = 8;                         // block-table entries in flight
-constexpr int kKvDmaPerWave = 2 * (kTileBytes / 1024) / kWaves;  // 4
-constexpr float kTau = 8.0f;                       // log2 headroom before the running max moves
+constexpr int kMaxBatch = 1024;     // sequences per launch (prefix sums in LDS)
+constexpr int kQSlots = 8;          // segments per phase (their q rows in LDS)
+constexpr int kTable = 512;         // windows per table phase
+constexpr float kTau = 8.0f;        // log2 headroom before the running max moves
+constexpr uint32_t kOob = 0x80000000u;  // a buffer offset past every window's range
+constexpr int kRsrcFlags = 0x00020000;  // buffer descriptor word 3 for gfx9 raw loads
+
+// windows of loads in flight per wave: one. With 16 waves per CU that is 64 KB
+// per CU, about the amount the memory system serves best (deeper rings of 2-10
+// windows measured slower at every group size).
+constexpr int kDepth = 1;
 
 // LDS layout (bytes)
-constexpr int kCwOff = kStages * kStageBytes;                 // int cw[kMaxBatch + 1]: window prefix sums
-constexpr int kLenOff = kCwOff + ((kMaxBatch + 1) * 4 + 15) / 16 * 16;  // int len[kMaxBatch]
-constexpr int kWtotOff = kLenOff + kMaxBatch * 4;             // int wtot[kWaves] scan scratch
-constexpr int kPgOff = kWtotOff + kWaves * 4;                 // int pgring[kPgRing]
-constexpr int kPwOff = kPgOff + kPgRing * 4;                  // float pw[kWaves][8][kMaxGroup]
-constexpr int kLdsBytes = kPwOff + kWaves * 8 * kMaxGroup * 4;
-static_assert(kPwOff % 16 == 0, "p broadcast rows are read 16 bytes at a time");
-static_assert(kLdsBytes * kBlocksPerCu <= 160 * 1024, "kBlocksPerCu workgroups share the CU's LDS");
+constexpr int kCwOff = 0;                                       // int cw[kMaxBatch + 1]
+constexpr int kLenOff = ((kMaxBatch + 1) * 4 + 15) / 16 * 16;  // int len[kMaxBatch]
+constexpr int kWtotOff = kLenOff + kMaxBatch * 4;              // int wtot[kWaves]
+constexpr int kTabOff = kWtotOff + 64;                         // int pair tab[kTable]
+constexpr int kPwOff = kTabOff + kTable * 8;                   // float pw[kWaves][8][8] p rows
+constexpr int kQsOff = kPwOff + kWaves * 8 * 8 * 4;            // bf16 q[kQSlots][G][kD]
+// exchange ring slots: segments a wave may close ahead of the slowest wave
+template <int G>
+constexpr int xslots() { return G <= 4 ? 2 : 1; }
+template <int G>
+constexpr int xo_off() { return kQsOff + kQSlots * G * kD * 2; }  // float xo[R][kWaves][G][kD]
+template <int G>
+constexpr int xml_off() { return xo_off<G>() + xslots<G>() * kWaves * G * kD * 4; }  // float xml[R][kWaves][G][2]
+template <int G>
+constexpr int xsync_off() { return xml_off<G>() + xslots<G>() * kWaves * G * 2 * 4; }  // int cnt[R], gen[R]
+template <int G>
+constexpr int sfx_lds_bytes() { return xsync_off<G>() + 2 * xslots<G>() * 4; }
+static_assert(kTabOff % 16 == 0 && kPwOff % 16 == 0 && kQsOff % 16 == 0 && xo_off<1>() % 16 == 0 &&
+                  xo_off<3>() % 16 == 0 && xml_off<3>() % 8 == 0,
+              "aligned LDS rows");
+static_assert(sfx_lds_bytes<kMaxGroup>() <= 80 * 1024, "two workgroups per CU");
+
+// window table entry: x = page id (-1: not a valid page), y = packed fields
+constexpr int kTvBits = 7;  // valid tokens 1 .. 64
+__device__ __forceinline__ int tab_tv(int y) { return y & 127; }
+__device__ __forceinline__ bool tab_first(int y) { return (y >> 7) & 1; }
+__device__ __forceinline__ bool tab_last(int y) { return (y >> 8) & 1; }
+__device__ __forceinline__ int tab_odd(int y) { return (y >> 9) & 1; }  // window starts at page row 64
+__device__ __forceinline__ int tab_b(int y) { return y >> 10; }
 
 struct SuffixArgs {
     const uint16_t *q;
@@ -107,14 +160,15 @@ struct SuffixArgs {
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 // Every control used below (quad_perm, row_half_mirror, row_ror) reads a lane of
 // the same 16-lane row, so bound_ctrl never applies; setting it lets the
 // compiler fold the move into the consuming add (v_add_f32_dpp).
 #define CK_DPP(x, ctrl) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), ctrl, 0xF, 0xF, true))
 
-// op(x[l], x[l ^ 16]) and op(x[l], x[l ^ 32]) through v_permlane16_swap /
+// x[l] op x[l ^ 16] and x[l] op x[l ^ 32] through v_permlane16_swap /
 // v_permlane32_swap: swapping x with itself leaves x[l] in one result and the
 // partner lane's x in the other (a VALU exchange, no LDS round trip).
 __device__ __forceinline__ float max_xor16(float x) {
@@ -137,19 +191,30 @@ __device__ __forceinline__ float sum8(float x) {
     x += CK_DPP(x, 0x141);  // row_half_mirror: the other quad of the 8
     return x;
 }
-// Reduce a value that is constant within each 8-lane group over the 8 groups.
-__device__ __forceinline__ float max_groups(float x) {
-    x = fmaxf(x, CK_DPP(x, 0x128));  // row_ror:8, the other group of the 16-lane row
-    return max_xor32(max_xor16(x));
-}
-__device__ __forceinline__ float sum_groups(float x) {
-    x += CK_DPP(x, 0x128);
+// Sum / max over the 8 lanes l, l^8, l^16, ..., l^56 (the token slots of a wave).
+__device__ __forceinline__ float sum_slots(float x) {
+    x += CK_DPP(x, 0x128);  // row_ror:8: the other 8 of the 16-lane row
     return sum_xor32(sum_xor16(x));
+}
+__device__ __forceinline__ float max_slots(float x) {
+    x = fmaxf(x, CK_DPP(x, 0x128));
+    return max_xor32(max_xor16(x));
 }
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
                                            false);
+}
+// 16-dim bf16 dot product (two 8-dim halves, two chains)
+__device__ __forceinline__ float dot16(const u32x4 &k0, const u32x4 &k1, const u32x4 &q0, const u32x4 &q1) {
+    float d0 = dot2(k0[0], q0[0], 0.f), d1 = dot2(k1[0], q1[0], 0.f);
+    d0 = dot2(k0[1], q0[1], d0);
+    d1 = dot2(k1[1], q1[1], d1);
+    d0 = dot2(k0[2], q0[2], d0);
+    d1 = dot2(k1[2], q1[2], d1);
+    d0 = dot2(k0[3], q0[3], d0);
+    d1 = dot2(k1[3], q1[3], d1);
+    return d0 + d1;
 }
 
 __device__ __forceinline__ int64_t clamp_len(const SuffixArgs &a, int64_t kvl) {
@@ -160,64 +225,56 @@ __device__ __forceinline__ int64_t clamp_len(const SuffixArgs &a, int64_t kvl) {
     return kvl < 0 ? 0 : kvl;
 }
 
-// Walk over the windows of a workgroup's window range [w0, w1) of the list of
-// all windows; consecutive windows cross sequences. Values are wave-uniform.
-struct Cursor {
-    int b;       // sequence
-    int k;       // window index inside the sequence (tokens 64k ..)
-    int kfirst;  // first window of this workgroup's segment of b
-    int kend;    // one past the segment's last window
-    bool valid;
-};
-
-__device__ __forceinline__ void cursor_seg(Cursor &cur, const CK_LDS int *cw, int w0, int w1) {
-    const int base = cw[cur.b];
-    cur.k = (w0 > base ? w0 : base) - base;
-    const int e = cw[cur.b + 1];
-    cur.kend = (w1 < e ? w1 : e) - base;
-    cur.kfirst = cur.k;
-}
-
-__device__ __forceinline__ void cursor_next(Cursor &cur, const CK_LDS int *cw, int batch, int w0, int w1) {
-    if (!cur.valid) return;
-    if (++cur.k < cur.kend) return;
-    int b = cur.b + 1;
-    while (b < batch && cw[b + 1] == cw[b]) ++b;  // empty sequences have no windows
-    if (b >= batch || cw[b] >= w1) {
-        cur.valid = false;
-        return;
+// Largest b in [0, batch] with cw[b] <= x (the sequence holding window x < W).
+__device__ __forceinline__ int seq_of_window(const CK_LDS int *cw, int batch, int x) {
+    int lo = 0, hi = batch;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (cw[mid] <= x) lo = mid;
+        else hi = mid - 1;
     }
-    cur.b = b;
-    cursor_seg(cur, cw, w0, w1);
+    return lo;
 }
 
 template <int G>
-__global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
+__device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a) {
+    constexpr int D = kDepth;
+    constexpr int NB = D + 1;  // register ring slots: D windows in flight + the one in use
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
     CK_LDS char *smem = (CK_LDS char *)smem_raw;
     CK_LDS int *cw = (CK_LDS int *)(smem + kCwOff);
     CK_LDS int *len = (CK_LDS int *)(smem + kLenOff);
     CK_LDS int *wtot = (CK_LDS int *)(smem + kWtotOff);
-    CK_LDS int *pgring = (CK_LDS int *)(smem + kPgOff);
-    constexpr int kPwRow = (G + 3) / 4 * 4;  // floats per token in the broadcast rows
-    constexpr int kQWaves = (G * 16 + 63) / 64;  // waves whose lanes carry the q rows
+    CK_LDS i32x2 *tab = (CK_LDS i32x2 *)(smem + kTabOff);
+    CK_LDS char *qs = smem + kQsOff;
+    constexpr int R = xslots<G>();
+    CK_LDS float *xo = (CK_LDS float *)(smem + xo_off<G>());
+    CK_LDS float *xml = (CK_LDS float *)(smem + xml_off<G>());
+    CK_LDS int *xcnt = (CK_LDS int *)(smem + xsync_off<G>());  // waves counted into each slot
+    CK_LDS int *xgen = xcnt + R;                                  // merges completed in each slot
 
     const int tid = threadIdx.x;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
-    const int t = lane >> 3;  // token slot of this lane in the wave's 8 tokens
-    const int c = lane & 7;   // column pair: dims 8c.. and 64+8c..
+    const int t = lane >> 3;  // K: token slot, token 8 wid + t of each window
+    const int c = lane & 7;   // K: dims 8c .. 8c+7 and 64+8c .. 64+8c+7
+    const int hf = lane >> 5; // V: tokens hf, 2 + hf, 4 + hf, 6 + hf of the wave's 8
+    const int dd = lane & 31; // V: dims 4 dd .. 4 dd + 3
     const int g = blockIdx.x % a.kv_heads;  // kv head group: query heads g * G .. + G
     const int chunk = blockIdx.x / a.kv_heads;
     const int gk = g / a.kv_sub;            // the physical kv head they read
-    CK_LDS float *pw = (CK_LDS float *)(smem + kPwOff) + wid * 8 * kPwRow;
 
-    // ---- lengths and window prefix sums (4 sequences per thread, block scan) ------
-    int lv[4];
+    if (tid < R) {
+        xcnt[tid] = 0;
+        xgen[tid] = 0;
+    }
+
+    // ---- lengths and window prefix sums (2 sequences per thread, block scan) ------
+    int lv[2];
     int local = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int i = 4 * tid + j;
+    for (int j = 0; j < 2; ++j) {
+        const int i = 2 * tid + j;
         const int ln = i < a.batch ? (int)clamp_len(a, a.kv_seqlens[i]) : 0;
         if (i < a.batch) len[i] = ln;
         lv[j] = (ln + kWin - 1) / kWin;
@@ -235,8 +292,8 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
     for (int ww = 0; ww < wid; ++ww) wave_off += wtot[ww];
     int run = wave_off + x - local;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int i = 4 * tid + j;
+    for (int j = 0; j < 2; ++j) {
+        const int i = 2 * tid + j;
         run += lv[j];
         if (i < a.batch) cw[i + 1] = run;
     }
@@ -250,263 +307,296 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_kernel(SuffixArgs a) {
     const int w1 = (int)((int64_t)(chunk + 1) * W / a.chunks);
     if (w0 >= w1) return;  // uniform over the workgroup
 
-    // first sequence: largest b with cw[b] <= w0 (then cw[b + 1] > w0)
-    int lo = 0, hi = a.batch;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (cw[mid] <= w0) lo = mid;
-        else hi = mid - 1;
-    }
-    Cursor cc;
-    cc.b = lo;
-    cc.valid = true;
-    cursor_seg(cc, cw, w0, w1);
-
-    // page ids of the first kStages - 1 windows; later ones travel with the ring
-    Cursor pc = cc;
-    for (int j = 0; j < kStages - 1; ++j) {
-        if (pc.valid && tid == j) pgring[j] = a.bt[(int64_t)pc.b * a.bt_cols + pc.k * kWin / kPage];
-        cursor_next(pc, cw, a.batch, w0, w1);
-    }
-    __syncthreads();
-
-    int tot = 0;  // vector-memory operations this wave has issued (wave-uniform)
-    // DMA group of window n (cursor cur): the block-table entry of window n + 3
-    // (cursor pcur; wave 0), the window's K and V rows, and on the first window
-    // of a segment the sequence's q rows.
-    auto issue = [&](const Cursor &cur, const Cursor &pcur, int n) {
-        CK_LDS char *kb = smem + (n % kStages) * kStageBytes;
-        CK_LDS char *vb = kb + kTileBytes;
-        CK_LDS char *qb = vb + kTileBytes;
-        if (wid == 0) {
-            const int32_t *psrc = pcur.valid ? a.bt + (int64_t)pcur.b * a.bt_cols + pcur.k * kWin / kPage : a.bt;
-            if (lane == 0) dma4(psrc, pgring + (n + kStages - 1) % kPgRing);
-            ++tot;
-        }
-        int page = pgring[n % kPgRing];
-        if (page < 0 || (int64_t)page >= a.num_blocks) page = 0;  // rows ignored at use
-        const int64_t pbase = (int64_t)page * a.page_stride + (int64_t)gk * a.head_off + (lane & 15) * 8;
-        const int t0 = (cur.k * kWin) % kPage + (lane >> 4);
+    // ---- q rows: the s-th segment of a phase in slot s ------------------------------
+    // The q rows of one sequence are G * 256 contiguous bytes: one or two wave DMAs.
+    auto dma_q = [&](int bq, int slot) {
 #pragma unroll
-        for (int j = 0; j < kKvDmaPerWave / 2; ++j) {
-            const int blk = wid * (kKvDmaPerWave / 2) + j;  // 4 token rows per DMA
-            const int64_t off = pbase + (int64_t)(t0 + blk * 4) * a.tok_stride;
-            dma16(a.k + off, kb + blk * 1024);
-            dma16(a.v + off, vb + blk * 1024);
+        for (int u0 = 0; u0 < G * 16; u0 += 64) {
+            if (u0 + lane < G * 16)
+                dma16(a.q + ((int64_t)bq * a.num_heads + g * G) * kD + (u0 + lane) * 8,
+                      qs + slot * G * (kD * 2) + u0 * 16);
         }
-        tot += kKvDmaPerWave;
-        if (cur.k == cur.kfirst && wid < kQWaves) {
-            if (wid * 64 + lane < G * 16)
-                dma16(a.q + ((int64_t)cur.b * a.num_heads + g * G) * kD + (wid * 64 + lane) * 8, qb + wid * 1024);
-            ++tot;
+    };
+    // the next non-empty sequence after b that starts inside [w0, w1), or -1
+    auto next_seg = [&](int b) {
+        ++b;
+        while (b < a.batch && cw[b + 1] == cw[b]) ++b;
+        return (b < a.batch && cw[b] < w1) ? b : -1;
+    };
+
+    // ---- per-lane constants ------------------------------------------------------------
+    const int64_t tokb = a.tok_stride * 2;                      // bytes between token rows
+    const uint32_t koff = (uint32_t)((8 * wid + t) * tokb + c * 16);   // K byte offset in a window
+    const uint32_t voff = (uint32_t)((8 * wid + hf) * tokb + dd * 8);  // V byte offset of token hf
+    const uint32_t win_bytes = (uint32_t)(kWin * tokb);          // a window's buffer range
+    const char *kbase = reinterpret_cast<const char *>(a.k) + (int64_t)gk * a.head_off * 2;
+    const char *vbase = reinterpret_cast<const char *>(a.v) + (int64_t)gk * a.head_off * 2;
+    const int64_t pgb = a.page_stride * 2;
+
+    float m[G], l[G], acc[G][4];
+    int nclose = 0;  // segments closed so far (exchange ring position)
+    int qslot = 0;   // segment of the current phase
+    u32x4 kbuf[NB][2];
+    u32x2 vbuf[NB][4];
+    constexpr int kPwRow = (G + 3) / 4 * 4;  // floats per token in this wave's p rows
+    static_assert(kPwRow <= 8, "p row");
+    CK_LDS float *pw = (CK_LDS float *)(smem + kPwOff) + wid * 64;
+
+    // K/V loads of the window with table entry e (e[0] < 0: invalid page; a dummy
+    // entry past the phase end has e[1] = 0, no valid tokens) into one ring slot
+    auto issue = [&](i32x2 e, u32x4 &k0, u32x4 &k1, u32x2 *vv) __attribute__((always_inline)) {
+        const int page = __builtin_amdgcn_readfirstlane(e[0]);
+        const int ey = __builtin_amdgcn_readfirstlane(e[1]);
+        const int64_t off = (int64_t)(page < 0 ? 0 : page) * pgb + (int64_t)(tab_odd(ey) * kWin) * tokb;
+        const int range = page < 0 ? 0 : (int)win_bytes;
+        const __amdgpu_buffer_rsrc_t rk =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(kbase + off), (short)0, range, kRsrcFlags);
+        const __amdgpu_buffer_rsrc_t rv =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(vbase + off), (short)0, range, kRsrcFlags);
+        const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
+        const uint32_t o = t < t1 ? koff : kOob;
+        k0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)o, 0, 0));
+        k1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)(o + 128), 0, 0));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t ov = 2 * j + hf < t1 ? voff + (uint32_t)(2 * j * tokb) : kOob;
+            vv[j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)ov, 0, 0));
         }
     };
 
-    // tot right after issuing each group still in flight (oldest first)
-    int gend[kStages - 1];
-#pragma unroll
-    for (int j = 0; j < kStages - 1; ++j) gend[j] = 0;
-    auto shift_gend = [&]() {
-#pragma unroll
-        for (int j = 0; j + 1 < kStages - 1; ++j) gend[j] = gend[j + 1];
-        gend[kStages - 2] = tot;
-    };
-    Cursor ic = cc;
-    for (int j = 0; j < kStages - 1; ++j) {
-        if (ic.valid) issue(ic, pc, j);
-        shift_gend();
-        cursor_next(ic, cw, a.batch, w0, w1);
-        cursor_next(pc, cw, a.batch, w0, w1);
-    }
-    // after the prologue gend[] holds groups 0 .. kStages - 2
+    // One window of a phase: issue window n + D into the slot freed last step,
+    // compute window n from slot J = n % NB, close its segment if it ends here.
+    auto step = [&](auto jc, int n, int np) __attribute__((always_inline)) {
+        constexpr int J = decltype(jc)::value;
+        constexpr int JI = (J + D) % NB;  // slot of window n + D (freed by window n - 1)
+        const int ni = n + D;
+        const i32x2 ei = ni < np ? tab[ni] : i32x2{-1, 0};
+        issue(ei, kbuf[JI][0], kbuf[JI][1], vbuf[JI]);
 
-    uint32_t qr[G][8];
-    float m[G], mu[G], thr[G], l[G], acc[G][2];  // mu = m, or 0 while m = -inf
-    int n_done = 0;
-    while (cc.valid) {
-        // everything issued after this window's group may stay in flight
-        const int after = __builtin_amdgcn_readfirstlane(tot - gend[0]);
-        if constexpr (kStages == 2) {
-            // only the previous segment close's two stores (waves wid < G) can
-            // follow the group of this window: two compares, not a 21-way switch
-            if (after >= 2) wait_vmcnt<2>();
-            else if (after == 1) wait_vmcnt<1>();
-            else wait_vmcnt<0>();
-        } else {
-            wait_vmcnt_dyn(after);
-        }
-        __syncthreads();
-        const int st = n_done % kStages;
-        // the next group goes into the stage consumed last iteration; half the
-        // waves issue before computing and half after, so the address unit
-        // drains one half's DMAs while the other half computes
-        const bool early = wid < kWaves / 2;
-        if (early && ic.valid) issue(ic, pc, n_done + kStages - 1);
-
-        CK_LDS char *kb = smem + st * kStageBytes;
-        CK_LDS char *vb = kb + kTileBytes;
-        CK_LDS char *qb = vb + kTileBytes;
-        const int b = cc.b;
-        const int thi = min(kWin, len[b] - cc.k * kWin);  // tokens of this window
-        const bool first = cc.k == cc.kfirst;
-        const bool last = cc.k + 1 == cc.kend;
-        const int praw = pgring[n_done % kPgRing];
-        const bool page_ok = praw >= 0 && (int64_t)praw < a.num_blocks;
-        if (first) {
+        const int ey = __builtin_amdgcn_readfirstlane(tab[n][1]);
+        const int b = tab_b(ey);
+        const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
+        if (tab_first(ey)) {
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                const u32x4 q0 = *reinterpret_cast<const CK_LDS u32x4 *>(qb + h * 256 + c * 16);
-                const u32x4 q1 = *reinterpret_cast<const CK_LDS u32x4 *>(qb + h * 256 + 128 + c * 16);
-                qr[h][0] = q0[0]; qr[h][1] = q0[1]; qr[h][2] = q0[2]; qr[h][3] = q0[3];
-                qr[h][4] = q1[0]; qr[h][5] = q1[1]; qr[h][6] = q1[2]; qr[h][7] = q1[3];
                 m[h] = -INFINITY;
-                mu[h] = 0.f;
-                thr[h] = -INFINITY;
                 l[h] = 0.f;
-                acc[h][0] = 0.f;
-                acc[h][1] = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[h][e] = 0.f;
             }
         }
-
-        // this wave's tokens 8 * wid + [0, t1)
-        const int t1 = min(8, thi - 8 * wid);
         if (t1 > 0) {
-            const int tt = 8 * wid + t;
-            const u32x4 k0 = *reinterpret_cast<const CK_LDS u32x4 *>(kb + tt * 256 + c * 16);
-            const u32x4 k1 = *reinterpret_cast<const CK_LDS u32x4 *>(kb + tt * 256 + 128 + c * 16);
-            const uint32_t kr[8] = {k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
-            const bool tok_ok = t < t1;
-            float s[G];
+            const CK_LDS char *qrow = qs + qslot * G * (kD * 2) + c * 16;
+            const u32x4 k0 = kbuf[J][0], k1 = kbuf[J][1];
+            float s[G];  // scores, then p in place
             bool trig = false;
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                float d0 = dot2(kr[0], qr[h][0], 0.f);
-                float d1 = dot2(kr[4], qr[h][4], 0.f);
-#pragma unroll
-                for (int e = 1; e < 4; ++e) {
-                    d0 = dot2(kr[e], qr[h][e], d0);
-                    d1 = dot2(kr[4 + e], qr[h][4 + e], d1);
-                }
-                float d = sum8(d0 + d1);
-                d = page_ok ? d : 0.f;  // an invalid page reads as zero rows
-                s[h] = tok_ok ? d * a.scale_log2 : -INFINITY;
-                trig |= s[h] > thr[h];
+                const u32x4 q0 = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2));
+                const u32x4 q1 = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2) + 128);
+                s[h] = sum8(dot16(k0, k1, q0, q1)) * a.scale_log2;
             }
+            if (t1 < 8) {
+#pragma unroll
+                for (int h = 0; h < G; ++h) s[h] = t < t1 ? s[h] : -INFINITY;
+            }
+#pragma unroll
+            for (int h = 0; h < G; ++h) trig |= s[h] > m[h] + kTau;  // m = -inf: always
             if (__builtin_amdgcn_ballot_w64(trig)) {
-                // some score passed its head's headroom: move the reference maxima
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
-                    const float m_new = fmaxf(m[h], max_groups(s[h]));
+                    const float m_new = fmaxf(m[h], max_slots(s[h]));
                     if (m_new > m[h]) {
                         const float f = exp2_fast(m[h] - m_new);  // 0 from -inf
-                        acc[h][0] *= f;
-                        acc[h][1] *= f;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[h][e] *= f;
                         l[h] *= f;
                         m[h] = m_new;
-                        mu[h] = m_new;  // > -inf here
-                        thr[h] = m_new + kTau;
                     }
                 }
             }
-            float p[kPwRow];
-#pragma unroll
-            for (int h = 0; h < kPwRow; ++h) p[h] = 0.f;
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                p[h] = exp2_fast(s[h] - mu[h]);  // 0 for masked tokens
-                l[h] += p[h];
+                s[h] = exp2_fast(s[h] - (m[h] == -INFINITY ? 0.f : m[h]));  // 0 for masked tokens
+                l[h] += s[h];
             }
+            // p of token t -> this wave's row t (lanes c = 0), read back per V token
             if (c == 0) {
 #pragma unroll
                 for (int h4 = 0; h4 < kPwRow; h4 += 4)
-                    *reinterpret_cast<CK_LDS f32x4 *>(pw + t * kPwRow + h4) =
-                        f32x4{p[h4], p[h4 + 1], p[h4 + 2], p[h4 + 3]};
+                    *reinterpret_cast<CK_LDS f32x4 *>(pw + t * 8 + h4) =
+                        f32x4{s[h4], h4 + 1 < G ? s[h4 + 1] : 0.f, h4 + 2 < G ? s[h4 + 2] : 0.f,
+                              h4 + 3 < G ? s[h4 + 3] : 0.f};
             }
-            if (page_ok) {
-                // acc[h][dims 2*lane, 2*lane + 1] += p[token][h] * V[token]
-                auto pv_token = [&](int j) {
-                    const uint32_t vv =
-                        *reinterpret_cast<const CK_LDS uint32_t *>(vb + (8 * wid + j) * 256 + lane * 4);
-                    const float v0 = bf16_lo(vv), v1 = bf16_hi(vv);
 #pragma unroll
-                    for (int h4 = 0; h4 < kPwRow; h4 += 4) {
-                        const f32x4 pv = *reinterpret_cast<const CK_LDS f32x4 *>(pw + j * kPwRow + h4);
+            for (int j = 0; j < 4; ++j) {
+                const u32x2 vv = vbuf[J][j];
+                const float v0 = bf16_lo(vv[0]), v1 = bf16_hi(vv[0]), v2 = bf16_lo(vv[1]), v3 = bf16_hi(vv[1]);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            if (h4 + e < G) {
-                                acc[h4 + e][0] = fmaf(pv[e], v0, acc[h4 + e][0]);
-                                acc[h4 + e][1] = fmaf(pv[e], v1, acc[h4 + e][1]);
-                            }
+                for (int h4 = 0; h4 < kPwRow; h4 += 4) {
+                    const f32x4 pv = *reinterpret_cast<const CK_LDS f32x4 *>(pw + (2 * j + hf) * 8 + h4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (h4 + e < G) {
+                            acc[h4 + e][0] = fmaf(pv[e], v0, acc[h4 + e][0]);
+                            acc[h4 + e][1] = fmaf(pv[e], v1, acc[h4 + e][1]);
+                            acc[h4 + e][2] = fmaf(pv[e], v2, acc[h4 + e][2]);
+                            acc[h4 + e][3] = fmaf(pv[e], v3, acc[h4 + e][3]);
                         }
                     }
-                };
-                if (t1 == 8) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) pv_token(j);
-                } else {
-                    for (int j = 0; j < t1; ++j) pv_token(j);
                 }
             }
         }
 
-        if (!early && ic.valid) issue(ic, pc, n_done + kStages - 1);
-        shift_gend();
-        cursor_next(ic, cw, a.batch, w0, w1);
-        cursor_next(pc, cw, a.batch, w0, w1);
-
-        if (last) {
-            // ---- close the segment: per-wave sums, then the 8 waves through LDS ----
+        if (tab_last(ey)) {
+            // ---- close the segment ---------------------------------------------------
 #pragma unroll
-            for (int h = 0; h < G; ++h) l[h] = sum_groups(l[h]);  // token-slot partials
-            __syncthreads();  // every wave is done with this stage (q is in registers)
-            CK_LDS float *xacc = (CK_LDS float *)kb;    // [kWaves][G][kD]
-            CK_LDS float *xm = xacc + kWaves * G * kD;  // [kWaves][G]
-            CK_LDS float *xl = xm + kWaves * G;         // [kWaves][G]
+            for (int h = 0; h < G; ++h) {
+                l[h] = sum_slots(l[h]);
 #pragma unroll
-            for (int h = 0; h < G; ++h)
-                *reinterpret_cast<CK_LDS f32x2 *>(xacc + (wid * G + h) * kD + 2 * lane) = f32x2{acc[h][0], acc[h][1]};
+                for (int e = 0; e < 4; ++e) acc[h][e] = sum_xor32(acc[h][e]);  // the two half-waves
+            }
+            const int r = nclose % R;
+            const int want = nclose / R;  // merges the slot has seen before this segment
+            // the slot's previous segment must be merged (bounded: a wait that never
+            // ended would mean a broken invariant, and results then are wrong, not hung)
+            for (int spin = 0; *(volatile CK_LDS int *)(xgen + r) != want && spin < (1 << 22); ++spin)
+                __builtin_amdgcn_s_sleep(1);
+            CK_LDS float *xo_r = xo + r * kWaves * G * kD;
+            CK_LDS float *xml_r = xml + r * kWaves * G * 2;
+            if (hf == 0) {
+#pragma unroll
+                for (int h = 0; h < G; ++h)
+                    *reinterpret_cast<CK_LDS f32x4 *>(xo_r + (wid * G + h) * kD + 4 * dd) =
+                        f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+            }
             if (lane == 0) {
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
-                    xm[wid * G + h] = m[h];
-                    xl[wid * G + h] = l[h];
+                    xml_r[(wid * G + h) * 2] = m[h];
+                    xml_r[(wid * G + h) * 2 + 1] = l[h];
                 }
             }
-            __syncthreads();
-            if (wid < G) {
-                const int h = wid;
-                float mx = -INFINITY;
+            // a wave's LDS operations complete in order: its rows are in before it counts itself
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            int old = 0;
+            if (lane == 0) old = __hip_atomic_fetch_add(xcnt + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            old = __builtin_amdgcn_readfirstlane(old);
+            if (old == kWaves - 1) {
+                // the last wave in: merge the 8 partials of every query head
+                asm volatile("" ::: "memory");
+#pragma unroll 1
+                for (int u0 = 0; u0 < 32 * G; u0 += 64) {
+                    const int u = u0 + lane;
+                    if (u < 32 * G) {
+                        const int h = u >> 5, d4 = u & 31;
+                        float mx = -INFINITY;
 #pragma unroll
-                for (int ww = 0; ww < kWaves; ++ww) mx = fmaxf(mx, xm[ww * G + h]);
-                const float mu = mx == -INFINITY ? 0.f : mx;
-                float lt = 0.f, o0 = 0.f, o1 = 0.f;
+                        for (int ww = 0; ww < kWaves; ++ww) mx = fmaxf(mx, xml_r[(ww * G + h) * 2]);
+                        const float mz = mx == -INFINITY ? 0.f : mx;
+                        float lt = 0.f;
+                        f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int ww = 0; ww < kWaves; ++ww) {
-                    const float f = exp2_fast(xm[ww * G + h] - mu);
-                    lt = fmaf(xl[ww * G + h], f, lt);
-                    const f32x2 xa = *reinterpret_cast<const CK_LDS f32x2 *>(xacc + (ww * G + h) * kD + 2 * lane);
-                    o0 = fmaf(xa[0], f, o0);
-                    o1 = fmaf(xa[1], f, o1);
+                        for (int ww = 0; ww < kWaves; ++ww) {
+                            const float f = exp2_fast(xml_r[(ww * G + h) * 2] - mz);
+                            lt = fmaf(xml_r[(ww * G + h) * 2 + 1], f, lt);
+                            const f32x4 xa =
+                                *reinterpret_cast<const CK_LDS f32x4 *>(xo_r + (ww * G + h) * kD + 4 * d4);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) o[e] = fmaf(xa[e], f, o[e]);
+                        }
+                        const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+                        const float lse_v = lt > 0.f ? (mx + __log2f(lt)) * kLn2 : -INFINITY;
+                        const bool head_part = cw[b] < w0;
+                        const bool tail_part = cw[b + 1] > w1;
+                        if (!head_part && !tail_part) {
+                            const int64_t row = (int64_t)b * a.num_heads + g * G + h;
+                            *reinterpret_cast<uint2 *>(a.out + row * kD + 4 * d4) = make_uint2(
+                                pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv));
+                            if (d4 == 0) a.lse[row] = lse_v;
+                        } else {
+                            const int64_t pidx =
+                                (((int64_t)g * a.chunks + chunk) * 2 + (head_part ? 0 : 1)) * G + h;
+                            *reinterpret_cast<float4 *>(a.part_o + pidx * kD + 4 * d4) =
+                                make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+                            if (d4 == 0) a.part_lse[pidx] = lse_v;
+                        }
+                    }
                 }
-                const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-                const float lse_v = lt > 0.f ? (mx + __log2f(lt)) * kLn2 : -INFINITY;
-                const bool head_part = cw[b] < w0;
-                const bool tail_part = cw[b + 1] > w1;
-                if (!head_part && !tail_part) {
-                    const int64_t row = (int64_t)b * a.num_heads + g * G + h;
-                    *reinterpret_cast<uint32_t *>(a.out + row * kD + 2 * lane) = pack_bf16x2(o0 * inv, o1 * inv);
-                    if (lane == 0) a.lse[row] = lse_v;
-                } else {
-                    const int64_t pidx = (((int64_t)g * a.chunks + chunk) * 2 + (head_part ? 0 : 1)) * G + h;
-                    *reinterpret_cast<float2 *>(a.part_o + pidx * kD + 2 * lane) = make_float2(o0 * inv, o1 * inv);
-                    if (lane == 0) a.part_lse[pidx] = lse_v;
-                }
-                tot += 2;  // one O store and one LSE store
+                // free the slot: reset its count, then publish the merge
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                if (lane == 0) xcnt[r] = 0;
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                if (lane == 0) xgen[r] = want + 1;
             }
+            ++nclose;
+            ++qslot;
         }
-        ++n_done;
-        cursor_next(cc, cw, a.batch, w0, w1);
+    };
+
+    // ---- phases of up to kTable windows and kQSlots segments: table and q rows,
+    //      prologue loads, streaming loop --------------------------------------------
+    const int nwin = w1 - w0;
+    for (int p0 = 0; p0 < nwin;) {
+        if (p0 > 0) {
+            wait_vmcnt<0>();
+            __syncthreads();  // every wave is done with the previous phase's table and q rows
+        }
+        int bq = seq_of_window(cw, a.batch, w0 + p0);  // the phase's first segment
+        int nseg = 0;
+        while (bq >= 0 && nseg < kQSlots) {
+            if (nseg % kWaves == wid) dma_q(bq, nseg);
+            ++nseg;
+            bq = next_seg(bq);
+        }
+        int p1 = min(p0 + kTable, nwin);
+        if (bq >= 0) p1 = min(p1, cw[bq] - w0);  // the next segment opens the next phase
+        const int np = p1 - p0;
+        for (int i = tid; i < np; i += kThreads) {
+            const int wg = w0 + p0 + i;
+            const int b = seq_of_window(cw, a.batch, wg);
+            const int k = wg - cw[b];
+            const int tv = min(len[b] - k * kWin, kWin);
+            const int first = wg == max(cw[b], w0);
+            const int last = wg == min(cw[b + 1], w1) - 1;
+            const int page = a.bt[(int64_t)b * a.bt_cols + (k >> 1)];
+            const bool ok = page >= 0 && (int64_t)page < a.num_blocks;
+            tab[i] = i32x2{ok ? page : -1, tv | (first << 7) | (last << 8) | ((k & 1) << 9) | (b << 10)};
+        }
+        wait_vmcnt<0>();  // q rows and page ids in
+        __syncthreads();
+        qslot = 0;
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            const i32x2 e = j < np ? tab[j] : i32x2{-1, 0};
+            issue(e, kbuf[j][0], kbuf[j][1], vbuf[j]);
+        }
+        // full rounds of NB steps, then the rest: the ring slot of every step is a
+        // compile-time constant and no step leaves the loop early, so the
+        // compiler's vmcnt bookkeeping sees one path around the back edge
+        int n = 0;
+        for (int it = np / NB; it > 0; --it) {
+            static_for<NB>([&](auto jc) __attribute__((always_inline)) { step(jc, n + decltype(jc)::value, np); });
+            n += NB;
+        }
+        const int rem = np - n;
+        static_for<NB>([&](auto jc) __attribute__((always_inline)) {
+            if (decltype(jc)::value < rem) step(jc, n + decltype(jc)::value, np);
+        });
+        p0 = p1;
     }
+}
+
+// Up to 4 query heads per group the body fits in 128 registers: 4 waves per
+// SIMD, two workgroups per CU. Above, its per-head state needs more, and the
+// grid's second half runs as the first half's workgroups finish.
+template <int G>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void suffix_stream_kernel(SuffixArgs a) {
+    suffix_stream_body<G>(a);
+}
+template <int G>
+__global__ __launch_bounds__(kThreads) void suffix_stream_wide_kernel(SuffixArgs a) {
+    suffix_stream_body<G>(a);
 }
 
 // Chunk that owns window p: chunk c covers windows [c*W/P, (c+1)*W/P).
@@ -744,11 +834,18 @@ int64_t group_parts(int64_t num_heads, int64_t chunks) { return num_heads * chun
 template <int G>
 int launch_suffix(const SuffixArgs &a, bool fixup, const EpilogueArgs *epi, hipStream_t st) {
     static std::atomic<uint64_t> lds_set{0};
-    int rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&suffix_stream_kernel<G>), kLdsBytes, lds_set);
+    constexpr int kLds = sfx_lds_bytes<G>();
+    const void *fn;
+    if constexpr (G <= 4) fn = reinterpret_cast<const void *>(&suffix_stream_kernel<G>);
+    else fn = reinterpret_cast<const void *>(&suffix_stream_wide_kernel<G>);
+    int rc = ensure_dynamic_lds(fn, kLds, lds_set);
     if (rc != CK_OK) return rc;
-    static_assert((kWaves * G * kD + 2 * kWaves * G) * 4 <= kStageBytes, "exchange fits in a stage");
-    hipLaunchKernelGGL(suffix_stream_kernel<G>, dim3((unsigned)(a.kv_heads * a.chunks)), dim3(kThreads), kLdsBytes,
-                       st, a);
+    if constexpr (G <= 4)
+        hipLaunchKernelGGL(suffix_stream_kernel<G>, dim3((unsigned)(a.kv_heads * a.chunks)), dim3(kThreads), kLds,
+                           st, a);
+    else
+        hipLaunchKernelGGL(suffix_stream_wide_kernel<G>, dim3((unsigned)(a.kv_heads * a.chunks)), dim3(kThreads),
+                           kLds, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
     if (fixup)
@@ -790,15 +887,12 @@ int64_t suffix_group_batch(int64_t kv_cap) {
     return n < 1 ? 1 : n;
 }
 
-// Workgroups per kv head group: the grid holds as many workgroups as can be resident
-// at once. Up to 5 query heads per kv head the stream kernel fits in 128 VGPRs
-// and kBlocksPerCu workgroups share a CU; 6-8 heads need more registers (the
-// per-head accumulators) and run one per CU, where a grid twice that size
-// would queue half its workgroups behind the first half.
+// Workgroups per kv head group: two resident workgroups per CU (16 waves of at
+// most 128 registers, under 80 KB of LDS each), so the grid holds 512
+// workgroups over all kv head groups and starts at once.
 int64_t suffix_default_chunks(int64_t num_heads, int64_t kv_heads) {
     const int64_t groups = kv_heads * suffix_sub_groups(num_heads, kv_heads);
-    const int64_t per_cu = num_heads / groups <= 5 ? kBlocksPerCu : 1;
-    const int64_t p = per_cu * 256 / groups;
+    const int64_t p = 512 / groups;
     return p > 0 ? p : 1;
 }
 
