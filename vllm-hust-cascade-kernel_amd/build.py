@@ -46,11 +46,14 @@ def run(cmd, cwd=None):
     return out
 
 
-# Per-source code-generation options. The stage-1 kernel keeps its score and
+# Per-source code-generation options. The stage-1 kernels keep their score and
 # output accumulators in architectural VGPRs (MFMA results written there, not
 # to AGPRs): the softmax reads and rescales them with VALU instructions every
 # 128 tokens, and AGPR-resident accumulators cost a copy in and out each time.
-SOURCE_FLAGS = {"fa_stage1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+# suffix_decode.hip holds the fused cascade kernel, whose stage-1 waves run the
+# same body.
+SOURCE_FLAGS = {"fa_stage1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+                "suffix_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def compile_hip(src):

@@ -43,7 +43,16 @@ constexpr int64_t kAlign = 256;
 
 int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
+// The fused kernel (stage-1 units and suffix chunks side by side) pays off while
+// stage-1 is no larger than the suffix side can hide; a prefix whose MFMA work
+// (kv heads x query rows of a kv head x prefix tokens) exceeds this runs the
+// kernels one after another, stage-1 with all its waves.
+constexpr int64_t kFusedMaxS1Work = (int64_t)1 << 26;
+constexpr int64_t kFusedUnits = 256;  // stage-1 units of the fused kernel (one per CU)
+
 struct CascadeLayout {
+    bool fused;
+    int64_t s1_units;     // fused: stage-1 units
     int64_t s1_splits;
     int64_t s1_bytes;     // stage-1 partials, or the final O1 [R][128] + padded LSE1 [R * 8]
     int64_t chunks;
@@ -61,17 +70,21 @@ int cascade_layout(int64_t batch, int64_t num_heads, int64_t kv_heads, int64_t h
     if (num_heads > (1 << 16)) return CK_E_INVALID_ARG;
     if (prefix_cap > ((int64_t)1 << 30) || suffix_cap > ((int64_t)1 << 30)) return CK_E_INVALID_ARG;
     const int64_t rows = batch * num_heads;
+    const int64_t per = ck::suffix_group_batch(suffix_cap);
+    L->group_batch = batch < per ? batch : per;
+    L->fused = batch > 0 && batch <= per && kv_heads * (rows / kv_heads) * prefix_cap <= kFusedMaxS1Work;
     int64_t s1 = 1, s1_ws = 0;
-    if (batch > 0) {
+    L->s1_units = 0;
+    if (L->fused) {
+        ck::stage1_fused_plan(batch, num_heads, kv_heads, prefix_cap, kFusedUnits, &L->s1_units, &s1, &s1_ws);
+    } else if (batch > 0) {
         int rc = ck_fa_fp32_stage1_plan(1, batch, num_heads, kv_heads, head_dim, prefix_cap, &s1, &s1_ws);
         if (rc != CK_OK) return rc;
     }
     L->s1_splits = s1;
     const int64_t final_bytes = rows * (kD + 8) * (int64_t)sizeof(float);
     L->s1_bytes = align_up(s1 > 1 ? s1_ws : final_bytes);
-    L->chunks = ck::suffix_default_chunks(num_heads, kv_heads);
-    const int64_t per = ck::suffix_group_batch(suffix_cap);
-    L->group_batch = batch < per ? batch : per;
+    L->chunks = L->fused ? ck::suffix_fused_chunks(num_heads, kv_heads) : ck::suffix_default_chunks(num_heads, kv_heads);
     L->sfx_bytes = align_up(ck::suffix_group_ws_bytes(L->group_batch, num_heads, kv_heads, L->chunks));
     L->whole_bytes = align_up(L->group_batch * num_heads * (kD * 2 + 4));
     L->total = batch > 0 ? L->s1_bytes + L->sfx_bytes + L->whole_bytes : 0;
@@ -126,14 +139,22 @@ extern "C" int ck_cascade_decode(const void *q, const void *prefix_k, const void
     char *whole_region = sfx_region + L.sfx_bytes;
     const int64_t rows = batch * num_heads;
 
-    // 1. stage-1 over the shared prefix, the B queries as one request (q_len = B)
+    // 1. stage-1 over the shared prefix, the B queries as one request (q_len = B):
+    //    its own launch, or the stage-1 role of the fused kernel
     float *o1 = reinterpret_cast<float *>(s1_region);
     float *l1 = o1 + rows * kD;
-    int64_t s1 = 1;
-    rc = ck::stage1_launch(q, prefix_k, prefix_v, prefix_block_table, prefix_bt_cols, nullptr, prefix_kv_seqlen,
-                           nullptr, 1, batch, batch, batch, num_heads, kv_heads, head_dim, prefix_num_blocks,
-                           block_size, scale, prefix_cap, L.s1_splits, o1, l1, s1_region, L.s1_bytes, false, st,
-                           &s1);
+    int64_t s1 = 1, units = 0;
+    ck::s1::Stage1Args fa;
+    if (L.fused) {
+        rc = ck::stage1_fused_args(q, prefix_k, prefix_v, prefix_block_table, prefix_bt_cols, prefix_kv_seqlen, batch,
+                                   num_heads, kv_heads, prefix_num_blocks, scale, prefix_cap, kFusedUnits, o1, l1,
+                                   s1_region, L.s1_bytes, &fa, &units, &s1);
+    } else {
+        rc = ck::stage1_launch(q, prefix_k, prefix_v, prefix_block_table, prefix_bt_cols, nullptr, prefix_kv_seqlen,
+                               nullptr, 1, batch, batch, batch, num_heads, kv_heads, head_dim, prefix_num_blocks,
+                               block_size, scale, prefix_cap, L.s1_splits, o1, l1, s1_region, L.s1_bytes, false, st,
+                               &s1);
+    }
     if (rc != CK_OK) return rc;
     ck::Stage1Result r1;
     r1.rows = rows;
@@ -149,7 +170,7 @@ extern "C" int ck_cascade_decode(const void *q, const void *prefix_k, const void
         rc = ck::suffix_launch_group(q, suffix_k, suffix_v, suffix_block_table, suffix_bt_cols, suffix_kv_seqlens,
                                      b0, nb, num_heads, kv_heads, suffix_num_blocks, suffix_kv_layout, scale,
                                      suffix_cap, L.chunks,
-                                     o2, l2, sfx_region, &r1, out, lse_out, st);
+                                     o2, l2, sfx_region, &r1, out, lse_out, st, L.fused ? &fa : nullptr, units);
         if (rc != CK_OK) return rc;
     }
     return CK_OK;

@@ -117,6 +117,37 @@ __device__ __forceinline__ float max_xor32(float x) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Workgroup barrier (the stand-alone kernels) and a barrier among the waves of
+// one role of a workgroup that runs two roles side by side: sense-free counting
+// on two LDS words (arrivals, generation). A wave reads the generation before it
+// counts itself in, so the generation cannot move before it has.
+struct WgBarrier {
+    __device__ __forceinline__ void sync() const { __syncthreads(); }
+};
+struct GroupBarrier {
+    CK_LDS int *cnt;
+    CK_LDS int *gen;
+    int n;  // waves of the group
+    __device__ __forceinline__ void sync() const {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS writes are done
+        const int g0 = __builtin_amdgcn_readfirstlane(*(volatile CK_LDS int *)gen);
+        int old = 0;
+        if (__lane_id() == 0) old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        old = __builtin_amdgcn_readfirstlane(old);
+        if (old == n - 1) {
+            if (__lane_id() == 0) {
+                *cnt = 0;
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                *(volatile CK_LDS int *)gen = g0 + 1;
+            }
+        } else {
+            for (int spin = 0; *(volatile CK_LDS int *)gen == g0 && spin < (1 << 24); ++spin)
+                __builtin_amdgcn_s_sleep(1);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+};
+
 // ---- XCD-aware block order ----------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (block b runs on XCD
 // b % 8). Remap so that consecutive logical work ids land on the same XCD and

@@ -16,10 +16,11 @@
 // instruction occupies its SIMD for 4 cycles; at 8 TB/s a CU receives about
 // 15 bytes per cycle, so every instruction per K/V byte counts).
 // * Suffix lengths vary widely (geometric in the benchmark), so the work is cut
-//   into windows of 64 tokens of one sequence (the last window of a sequence
-//   may be short), and workgroup (kv head group g, chunk c) takes the c-th 1/P
-//   of the list of all windows, crossing sequence boundaries: every workgroup
-//   streams the same number of windows and starts once. Two workgroups per CU.
+//   into windows of 8 tokens per streaming wave (64 tokens for the 8-wave
+//   kernel) of one sequence (the last window of a sequence may be short), and
+//   workgroup (kv head group g, chunk c) takes the c-th 1/P of the list of all
+//   windows, crossing sequence boundaries: every workgroup streams the same
+//   number of windows and starts once. Two workgroups per CU.
 // * Start-up: lengths -> window prefix sums (block scan in LDS), then a table
 //   of the workgroup's windows (page id, first token, valid tokens, sequence,
 //   segment start/end) built in parallel in one round trip that also copies
@@ -56,6 +57,12 @@
 //   result while the others go on. A wave waits for a ring slot only if it runs
 //   a whole ring ahead of the slowest wave, which itself never waits, so every
 //   wait ends.
+// * Cascade (stage 1 + suffix + merge): one fused kernel, one workgroup per CU.
+//   Waves 0-3 run the stage-1 body (MFMA, LDS tiles: matrix cores and LDS),
+//   waves 4-7 stream suffix windows (memory pipe and vector ALU); each role
+//   synchronises only its own four waves through an LDS counter barrier, so
+//   the two run side by side instead of one kernel after the other, and a
+//   small epilogue kernel merges the two results.
 // * The range is processed in phases of at most 512 windows and 8 segments.
 //   A phase starts with one round trip that fills the window table and copies
 //   the q rows of its segments into LDS (read per window, which costs far less
@@ -87,9 +94,8 @@ __device__ __forceinline__ void static_for(F &&f) {
 
 constexpr int kD = 128;
 constexpr int kPage = 128;
-constexpr int kWaves = 8;
+constexpr int kWaves = 8;           // waves of the stand-alone stream kernel
 constexpr int kThreads = kWaves * 64;
-constexpr int kWin = 64;            // tokens per window: 8 per wave
 constexpr int kMaxGroup = 8;
 constexpr int kMaxBatch = 1024;     // sequences per launch (prefix sums in LDS)
 constexpr int kQSlots = 8;          // segments per phase (their q rows in LDS)
@@ -98,41 +104,40 @@ constexpr float kTau = 8.0f;        // log2 headroom before the running max move
 constexpr uint32_t kOob = 0x80000000u;  // a buffer offset past every window's range
 constexpr int kRsrcFlags = 0x00020000;  // buffer descriptor word 3 for gfx9 raw loads
 
-// windows of loads in flight per wave: one. With 16 waves per CU that is 64 KB
-// per CU, about the amount the memory system serves best (deeper rings of 2-10
-// windows measured slower at every group size).
+// windows of loads in flight per wave: one in the stand-alone kernel (16 waves
+// per CU: 64 KB per CU, about the amount the memory system serves best; deeper
+// rings of 2-10 windows measured slower there), more in the fused cascade
+// kernel, whose 4 streaming waves per CU carry the CU's whole share.
 constexpr int kDepth = 1;
+constexpr int kFusedDepth = 4;
 
-// LDS layout (bytes)
-constexpr int kCwOff = 0;                                       // int cw[kMaxBatch + 1]
-constexpr int kLenOff = ((kMaxBatch + 1) * 4 + 15) / 16 * 16;  // int len[kMaxBatch]
-constexpr int kWtotOff = kLenOff + kMaxBatch * 4;              // int wtot[kWaves]
-constexpr int kTabOff = kWtotOff + 64;                         // int pair tab[kTable]
-constexpr int kPwOff = kTabOff + kTable * 8;                   // float pw[kWaves][8][8] p rows
-constexpr int kQsOff = kPwOff + kWaves * 8 * 8 * 4;            // bf16 q[kQSlots][G][kD]
-// exchange ring slots: segments a wave may close ahead of the slowest wave
-template <int G>
-constexpr int xslots() { return G <= 4 ? 2 : 1; }
-template <int G>
-constexpr int xo_off() { return kQsOff + kQSlots * G * kD * 2; }  // float xo[R][kWaves][G][kD]
-template <int G>
-constexpr int xml_off() { return xo_off<G>() + xslots<G>() * kWaves * G * kD * 4; }  // float xml[R][kWaves][G][2]
-template <int G>
-constexpr int xsync_off() { return xml_off<G>() + xslots<G>() * kWaves * G * 2 * 4; }  // int cnt[R], gen[R]
-template <int G>
-constexpr int sfx_lds_bytes() { return xsync_off<G>() + 2 * xslots<G>() * 4; }
-static_assert(kTabOff % 16 == 0 && kPwOff % 16 == 0 && kQsOff % 16 == 0 && xo_off<1>() % 16 == 0 &&
-                  xo_off<3>() % 16 == 0 && xml_off<3>() % 8 == 0,
-              "aligned LDS rows");
-static_assert(sfx_lds_bytes<kMaxGroup>() <= 80 * 1024, "two workgroups per CU");
+// LDS layout (bytes) of the stream body for G query heads per group and NW waves
+template <int G, int NW>
+struct SfxLds {
+    static constexpr int kCw = 0;                                        // int cw[kMaxBatch + 1]
+    static constexpr int kLen = ((kMaxBatch + 1) * 4 + 15) / 16 * 16;   // int len[kMaxBatch]
+    static constexpr int kWtot = kLen + kMaxBatch * 4;                   // int wtot[NW]
+    static constexpr int kTab = kWtot + 64;                              // int pair tab[kTable]
+    static constexpr int kPw = kTab + kTable * 8;                        // float pw[NW][8][8] p rows
+    static constexpr int kQs = kPw + NW * 8 * 8 * 4;                     // bf16 q[kQSlots][G][kD]
+    static constexpr int kX = G <= 4 ? 2 : 1;                            // exchange ring slots
+    static constexpr int kXo = kQs + kQSlots * G * kD * 2;               // float xo[kX][NW][G][kD]
+    static constexpr int kXml = kXo + kX * NW * G * kD * 4;              // float xml[kX][NW][G][2]
+    static constexpr int kXsync = kXml + kX * NW * G * 2 * 4;            // int cnt[kX], gen[kX]
+    static constexpr int kBar = kXsync + 2 * kX * 4;                     // int bar[2] (group barrier)
+    static constexpr int kBytes = (kBar + 8 + 15) / 16 * 16;
+    static_assert(kTab % 16 == 0 && kPw % 16 == 0 && kQs % 16 == 0 && kXo % 16 == 0 && kXml % 8 == 0,
+                  "aligned LDS rows");
+};
+static_assert(SfxLds<kMaxGroup, kWaves>::kBytes <= 80 * 1024, "two stand-alone workgroups per CU");
 
-// window table entry: x = page id (-1: not a valid page), y = packed fields
-constexpr int kTvBits = 7;  // valid tokens 1 .. 64
-__device__ __forceinline__ int tab_tv(int y) { return y & 127; }
+// window table entry: [0] = page id (-1: not a valid page), [1] = packed fields
+__device__ __forceinline__ int tab_tv(int y) { return y & 127; }  // valid tokens 1 .. 64
 __device__ __forceinline__ bool tab_first(int y) { return (y >> 7) & 1; }
 __device__ __forceinline__ bool tab_last(int y) { return (y >> 8) & 1; }
-__device__ __forceinline__ int tab_odd(int y) { return (y >> 9) & 1; }  // window starts at page row 64
-__device__ __forceinline__ int tab_b(int y) { return y >> 10; }
+__device__ __forceinline__ int tab_sub(int y) { return (y >> 9) & 3; }  // the window's quarter/half of its page
+__device__ __forceinline__ int tab_b(int y) { return y >> 11; }
+
 
 struct SuffixArgs {
     const uint16_t *q;
@@ -236,32 +241,36 @@ __device__ __forceinline__ int seq_of_window(const CK_LDS int *cw, int batch, in
     return lo;
 }
 
-template <int G>
-__device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a) {
-    constexpr int D = kDepth;
+// The stream body on NW waves (thread tid of the group's NW * 64) as workgroup lb
+// of a grid of a.kv_heads * a.chunks, with the group's LDS at smem and its own
+// barrier. Windows hold 8 NW tokens.
+template <int G, int NW, int D, class Bar>
+__device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS char *smem, int lb, int tid,
+                                                   const Bar &bar) {
     constexpr int NB = D + 1;  // register ring slots: D windows in flight + the one in use
-    extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-    CK_LDS char *smem = (CK_LDS char *)smem_raw;
-    CK_LDS int *cw = (CK_LDS int *)(smem + kCwOff);
-    CK_LDS int *len = (CK_LDS int *)(smem + kLenOff);
-    CK_LDS int *wtot = (CK_LDS int *)(smem + kWtotOff);
-    CK_LDS i32x2 *tab = (CK_LDS i32x2 *)(smem + kTabOff);
-    CK_LDS char *qs = smem + kQsOff;
-    constexpr int R = xslots<G>();
-    CK_LDS float *xo = (CK_LDS float *)(smem + xo_off<G>());
-    CK_LDS float *xml = (CK_LDS float *)(smem + xml_off<G>());
-    CK_LDS int *xcnt = (CK_LDS int *)(smem + xsync_off<G>());  // waves counted into each slot
-    CK_LDS int *xgen = xcnt + R;                                  // merges completed in each slot
+    constexpr int kThr = NW * 64;
+    constexpr int kWin = 8 * NW;         // tokens per window
+    constexpr int kWpp = kPage / kWin;   // windows per page
+    using L = SfxLds<G, NW>;
+    CK_LDS int *cw = (CK_LDS int *)(smem + L::kCw);
+    CK_LDS int *len = (CK_LDS int *)(smem + L::kLen);
+    CK_LDS int *wtot = (CK_LDS int *)(smem + L::kWtot);
+    CK_LDS i32x2 *tab = (CK_LDS i32x2 *)(smem + L::kTab);
+    CK_LDS char *qs = smem + L::kQs;
+    constexpr int R = L::kX;
+    CK_LDS float *xo = (CK_LDS float *)(smem + L::kXo);
+    CK_LDS float *xml = (CK_LDS float *)(smem + L::kXml);
+    CK_LDS int *xcnt = (CK_LDS int *)(smem + L::kXsync);  // waves counted into each slot
+    CK_LDS int *xgen = xcnt + R;                             // merges completed in each slot
 
-    const int tid = threadIdx.x;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int t = lane >> 3;  // K: token slot, token 8 wid + t of each window
     const int c = lane & 7;   // K: dims 8c .. 8c+7 and 64+8c .. 64+8c+7
     const int hf = lane >> 5; // V: tokens hf, 2 + hf, 4 + hf, 6 + hf of the wave's 8
     const int dd = lane & 31; // V: dims 4 dd .. 4 dd + 3
-    const int g = blockIdx.x % a.kv_heads;  // kv head group: query heads g * G .. + G
-    const int chunk = blockIdx.x / a.kv_heads;
+    const int g = lb % a.kv_heads;  // kv head group: query heads g * G .. + G
+    const int chunk = lb / a.kv_heads;
     const int gk = g / a.kv_sub;            // the physical kv head they read
 
     if (tid < R) {
@@ -269,12 +278,13 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a) {
         xgen[tid] = 0;
     }
 
-    // ---- lengths and window prefix sums (2 sequences per thread, block scan) ------
-    int lv[2];
+    // ---- lengths and window prefix sums (kPer sequences per thread, block scan) ----
+    constexpr int kPer = kMaxBatch / kThr;
+    int lv[kPer];
     int local = 0;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int i = 2 * tid + j;
+    for (int j = 0; j < kPer; ++j) {
+        const int i = kPer * tid + j;
         const int ln = i < a.batch ? (int)clamp_len(a, a.kv_seqlens[i]) : 0;
         if (i < a.batch) len[i] = ln;
         lv[j] = (ln + kWin - 1) / kWin;
@@ -287,20 +297,20 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a) {
         if (lane >= off) x += y;
     }
     if (lane == 63) wtot[wid] = x;
-    __syncthreads();
+    bar.sync();
     int wave_off = 0;
     for (int ww = 0; ww < wid; ++ww) wave_off += wtot[ww];
     int run = wave_off + x - local;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int i = 2 * tid + j;
+    for (int j = 0; j < kPer; ++j) {
+        const int i = kPer * tid + j;
         run += lv[j];
         if (i < a.batch) cw[i + 1] = run;
     }
     if (tid == 0) cw[0] = 0;
-    __syncthreads();
-    if (blockIdx.x == 0)
-        for (int i = tid; i <= a.batch; i += kThreads) a.cw_out[i] = cw[i];
+    bar.sync();
+    if (lb == 0)
+        for (int i = tid; i <= a.batch; i += kThr) a.cw_out[i] = cw[i];
 
     const int W = cw[a.batch];
     const int w0 = (int)((int64_t)chunk * W / a.chunks);
@@ -340,14 +350,14 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a) {
     u32x2 vbuf[NB][4];
     constexpr int kPwRow = (G + 3) / 4 * 4;  // floats per token in this wave's p rows
     static_assert(kPwRow <= 8, "p row");
-    CK_LDS float *pw = (CK_LDS float *)(smem + kPwOff) + wid * 64;
+    CK_LDS float *pw = (CK_LDS float *)(smem + L::kPw) + wid * 64;
 
     // K/V loads of the window with table entry e (e[0] < 0: invalid page; a dummy
     // entry past the phase end has e[1] = 0, no valid tokens) into one ring slot
     auto issue = [&](i32x2 e, u32x4 &k0, u32x4 &k1, u32x2 *vv) __attribute__((always_inline)) {
         const int page = __builtin_amdgcn_readfirstlane(e[0]);
         const int ey = __builtin_amdgcn_readfirstlane(e[1]);
-        const int64_t off = (int64_t)(page < 0 ? 0 : page) * pgb + (int64_t)(tab_odd(ey) * kWin) * tokb;
+        const int64_t off = (int64_t)(page < 0 ? 0 : page) * pgb + (int64_t)(tab_sub(ey) * kWin) * tokb;
         const int range = page < 0 ? 0 : (int)win_bytes;
         const __amdgpu_buffer_rsrc_t rk =
             __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(kbase + off), (short)0, range, kRsrcFlags);
@@ -462,8 +472,8 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a) {
             // ended would mean a broken invariant, and results then are wrong, not hung)
             for (int spin = 0; *(volatile CK_LDS int *)(xgen + r) != want && spin < (1 << 22); ++spin)
                 __builtin_amdgcn_s_sleep(1);
-            CK_LDS float *xo_r = xo + r * kWaves * G * kD;
-            CK_LDS float *xml_r = xml + r * kWaves * G * 2;
+            CK_LDS float *xo_r = xo + r * NW * G * kD;
+            CK_LDS float *xml_r = xml + r * NW * G * 2;
             if (hf == 0) {
 #pragma unroll
                 for (int h = 0; h < G; ++h)
@@ -482,7 +492,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a) {
             int old = 0;
             if (lane == 0) old = __hip_atomic_fetch_add(xcnt + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             old = __builtin_amdgcn_readfirstlane(old);
-            if (old == kWaves - 1) {
+            if (old == NW - 1) {
                 // the last wave in: merge the 8 partials of every query head
                 asm volatile("" ::: "memory");
 #pragma unroll 1
@@ -492,12 +502,12 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a) {
                         const int h = u >> 5, d4 = u & 31;
                         float mx = -INFINITY;
 #pragma unroll
-                        for (int ww = 0; ww < kWaves; ++ww) mx = fmaxf(mx, xml_r[(ww * G + h) * 2]);
+                        for (int ww = 0; ww < NW; ++ww) mx = fmaxf(mx, xml_r[(ww * G + h) * 2]);
                         const float mz = mx == -INFINITY ? 0.f : mx;
                         float lt = 0.f;
                         f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                        for (int ww = 0; ww < kWaves; ++ww) {
+                        for (int ww = 0; ww < NW; ++ww) {
                             const float f = exp2_fast(xml_r[(ww * G + h) * 2] - mz);
                             lt = fmaf(xml_r[(ww * G + h) * 2 + 1], f, lt);
                             const f32x4 xa =
@@ -540,31 +550,31 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a) {
     for (int p0 = 0; p0 < nwin;) {
         if (p0 > 0) {
             wait_vmcnt<0>();
-            __syncthreads();  // every wave is done with the previous phase's table and q rows
+            bar.sync();  // every wave is done with the previous phase's table and q rows
         }
         int bq = seq_of_window(cw, a.batch, w0 + p0);  // the phase's first segment
         int nseg = 0;
         while (bq >= 0 && nseg < kQSlots) {
-            if (nseg % kWaves == wid) dma_q(bq, nseg);
+            if (nseg % NW == wid) dma_q(bq, nseg);
             ++nseg;
             bq = next_seg(bq);
         }
         int p1 = min(p0 + kTable, nwin);
         if (bq >= 0) p1 = min(p1, cw[bq] - w0);  // the next segment opens the next phase
         const int np = p1 - p0;
-        for (int i = tid; i < np; i += kThreads) {
+        for (int i = tid; i < np; i += kThr) {
             const int wg = w0 + p0 + i;
             const int b = seq_of_window(cw, a.batch, wg);
             const int k = wg - cw[b];
             const int tv = min(len[b] - k * kWin, kWin);
             const int first = wg == max(cw[b], w0);
             const int last = wg == min(cw[b + 1], w1) - 1;
-            const int page = a.bt[(int64_t)b * a.bt_cols + (k >> 1)];
+            const int page = a.bt[(int64_t)b * a.bt_cols + k / kWpp];
             const bool ok = page >= 0 && (int64_t)page < a.num_blocks;
-            tab[i] = i32x2{ok ? page : -1, tv | (first << 7) | (last << 8) | ((k & 1) << 9) | (b << 10)};
+            tab[i] = i32x2{ok ? page : -1, tv | (first << 7) | (last << 8) | ((k % kWpp) << 9) | (b << 11)};
         }
         wait_vmcnt<0>();  // q rows and page ids in
-        __syncthreads();
+        bar.sync();
         qslot = 0;
 #pragma unroll
         for (int j = 0; j < D; ++j) {
@@ -592,11 +602,13 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a) {
 // grid's second half runs as the first half's workgroups finish.
 template <int G>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void suffix_stream_kernel(SuffixArgs a) {
-    suffix_stream_body<G>(a);
+    extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+    suffix_stream_body<G, kWaves, kDepth>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
 }
 template <int G>
 __global__ __launch_bounds__(kThreads) void suffix_stream_wide_kernel(SuffixArgs a) {
-    suffix_stream_body<G>(a);
+    extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+    suffix_stream_body<G, kWaves, kDepth>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
 }
 
 // Chunk that owns window p: chunk c covers windows [c*W/P, (c+1)*W/P).
@@ -825,6 +837,35 @@ __global__ __launch_bounds__(kMaxGroup * 32) void cascade_epilogue_kernel(Epilog
     if (d4 == 0) e.lse_out[row] = lse_v;
 }
 
+// Fused cascade kernel: workgroup i runs stage-1 unit i on waves 0-3 (the
+// 128-row body with a 3-slot ring) and suffix chunk i on waves 4-7 (the stream
+// body on 4 waves, 32-token windows), side by side on one CU: each SIMD holds
+// one MFMA wave and one streaming wave, which fill each other's stalls, and the
+// prefix pages and the suffix pages stream at the same time. Each role has its
+// own LDS region and its own barrier; neither waits for the other.
+constexpr int kFusedS1Lds = s1::wide_lds_bytes<3>();
+template <int G>
+constexpr int fused_lds_bytes() { return kFusedS1Lds + SfxLds<G, 4>::kBytes + 16; }
+static_assert(fused_lds_bytes<kMaxGroup>() <= 160 * 1024, "one fused workgroup per CU");
+
+template <int G>
+__global__ __launch_bounds__(512) void cascade_fused_kernel(s1::Stage1Args s1a, int n1, SuffixArgs sa, int n2) {
+    extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+    CK_LDS char *smem = (CK_LDS char *)smem_raw;
+    CK_LDS int *bars = (CK_LDS int *)(smem + kFusedS1Lds + SfxLds<G, 4>::kBytes);
+    if (threadIdx.x < 4) bars[threadIdx.x] = 0;
+    __syncthreads();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (wave < 4) {
+        if ((int)blockIdx.x < n1)
+            s1::stage1_wide_body<4, 3>(s1a, smem, blockIdx.x, n1, threadIdx.x, GroupBarrier{bars, bars + 1, 4});
+    } else {
+        if ((int)blockIdx.x < n2)
+            suffix_stream_body<G, 4, kFusedDepth>(sa, smem + kFusedS1Lds, blockIdx.x, threadIdx.x - 256,
+                                     GroupBarrier{bars + 2, bars + 3, 4});
+    }
+}
+
 int64_t ceil_div(int64_t x, int64_t y) { return (x + y - 1) / y; }
 
 // partial (O, LSE) slots: 2 per (query head, chunk) -- the same count for any
@@ -832,9 +873,25 @@ int64_t ceil_div(int64_t x, int64_t y) { return (x + y - 1) / y; }
 int64_t group_parts(int64_t num_heads, int64_t chunks) { return num_heads * chunks * 2; }
 
 template <int G>
+int launch_fused(const s1::Stage1Args &s1a, int64_t n1, const SuffixArgs &a, const EpilogueArgs &epi,
+                 hipStream_t st) {
+    static std::atomic<uint64_t> lds_set{0};
+    constexpr int kLds = fused_lds_bytes<G>();
+    int rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&cascade_fused_kernel<G>), kLds, lds_set);
+    if (rc != CK_OK) return rc;
+    const int64_t n2 = (int64_t)a.kv_heads * a.chunks;
+    const int64_t grid = n1 > n2 ? n1 : n2;
+    hipLaunchKernelGGL(cascade_fused_kernel<G>, dim3((unsigned)grid), dim3(512), kLds, st, s1a, (int)n1, a, (int)n2);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return static_cast<int>(e);
+    hipLaunchKernelGGL(cascade_epilogue_kernel<G>, dim3((unsigned)(a.batch * a.kv_heads)), dim3(32 * G), 0, st, epi);
+    CK_RETURN_LAUNCH();
+}
+
+template <int G>
 int launch_suffix(const SuffixArgs &a, bool fixup, const EpilogueArgs *epi, hipStream_t st) {
     static std::atomic<uint64_t> lds_set{0};
-    constexpr int kLds = sfx_lds_bytes<G>();
+    constexpr int kLds = SfxLds<G, kWaves>::kBytes;
     const void *fn;
     if constexpr (G <= 4) fn = reinterpret_cast<const void *>(&suffix_stream_kernel<G>);
     else fn = reinterpret_cast<const void *>(&suffix_stream_wide_kernel<G>);
@@ -896,6 +953,12 @@ int64_t suffix_default_chunks(int64_t num_heads, int64_t kv_heads) {
     return p > 0 ? p : 1;
 }
 
+int64_t suffix_fused_chunks(int64_t num_heads, int64_t kv_heads) {
+    const int64_t groups = kv_heads * suffix_sub_groups(num_heads, kv_heads);
+    const int64_t p = 256 / groups;
+    return p > 0 ? p : 1;
+}
+
 int64_t suffix_group_ws_bytes(int64_t nb, int64_t num_heads, int64_t kv_heads, int64_t chunks) {
     const int64_t parts = group_parts(num_heads, chunks);
     return parts * (kD + 1) * (int64_t)sizeof(float) + (nb + 1) * (int64_t)sizeof(int32_t) + 256;
@@ -905,7 +968,7 @@ int suffix_launch_group(const void *q, const void *k, const void *v, const int32
                         const int64_t *kv_seqlens, int64_t b0, int64_t nb, int64_t num_heads, int64_t kv_heads,
                         int64_t num_blocks, int64_t kv_layout, float scale, int64_t kv_cap, int64_t chunks,
                         void *out, float *lse, void *group_ws, const Stage1Result *cascade, void *final_out,
-                        float *final_lse, hipStream_t stream) {
+                        float *final_lse, hipStream_t stream, const s1::Stage1Args *fused, int64_t fused_units) {
     const int64_t sub = suffix_sub_groups(num_heads, kv_heads);
     const int64_t G = num_heads / kv_heads / sub;  // query heads per workgroup
     const int64_t parts = group_parts(num_heads, chunks);
@@ -947,6 +1010,18 @@ int suffix_launch_group(const void *q, const void *k, const void *v, const int32
         e.num_heads = (int)num_heads;
         e.kv_heads = a.kv_heads;
         e.chunks = (int)chunks;
+    }
+    if (fused && cascade) {
+        switch (G) {
+            case 1: return launch_fused<1>(*fused, fused_units, a, e, stream);
+            case 2: return launch_fused<2>(*fused, fused_units, a, e, stream);
+            case 3: return launch_fused<3>(*fused, fused_units, a, e, stream);
+            case 4: return launch_fused<4>(*fused, fused_units, a, e, stream);
+            case 5: return launch_fused<5>(*fused, fused_units, a, e, stream);
+            case 6: return launch_fused<6>(*fused, fused_units, a, e, stream);
+            case 7: return launch_fused<7>(*fused, fused_units, a, e, stream);
+            default: return launch_fused<8>(*fused, fused_units, a, e, stream);
+        }
     }
     const bool fixup = cascade == nullptr;
     const EpilogueArgs *ep = cascade ? &e : nullptr;
@@ -1007,7 +1082,7 @@ extern "C" int ck_suffix_decode(const void *q, const void *k, const void *v, con
         const int64_t nb = batch - b0 < per_launch ? batch - b0 : per_launch;
         rc = suffix_launch_group(q, k, v, block_table, bt_cols, kv_seqlens, b0, nb, num_heads, kv_heads,
                                  num_blocks, kv_layout, scale, kv_cap, chunks, static_cast<uint16_t *>(out) + b0 * num_heads * kD,
-                                 lse + b0 * num_heads, workspace, nullptr, nullptr, nullptr, st);
+                                 lse + b0 * num_heads, workspace, nullptr, nullptr, nullptr, st, nullptr, 0);
         if (rc != CK_OK) return rc;
     }
     return CK_OK;
