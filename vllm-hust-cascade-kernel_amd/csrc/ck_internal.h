@@ -49,8 +49,8 @@ struct Stage1Result {
     int splits;
 };
 
-// Chunks per kv head group of the suffix role of the fused cascade kernel (one
-// fused workgroup per CU).
+// Chunks per kv head group of the fused cascade kernel: a pair per fused
+// workgroup (one workgroup per CU), one for each of its two roles.
 int64_t suffix_fused_chunks(int64_t num_heads, int64_t kv_heads);
 
 // Suffix kernels for sequences [b0, b0 + nb) of a batch (nb <= suffix_group_batch).

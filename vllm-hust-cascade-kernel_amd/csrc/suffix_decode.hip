@@ -110,6 +110,10 @@ constexpr int kRsrcFlags = 0x00020000;  // buffer descriptor word 3 for gfx9 raw
 // kernel, whose 4 streaming waves per CU carry the CU's whole share.
 constexpr int kDepth = 1;
 constexpr int kFusedDepth = 4;
+constexpr int kFusedTokDepth = 3;  // token-major: 16 registers per window and lane
+// Share of each fused workgroup's suffix windows that its streaming waves take
+// (in 1/256); the stage-1 waves take the rest after their stage-1 unit.
+constexpr int kFusedSplit = 192;
 
 // LDS layout (bytes) of the stream body for G query heads per group and NW waves
 template <int G, int NW>
@@ -160,8 +164,40 @@ struct SuffixArgs {
     int kv_heads;  // kv head groups of the grid: physical kv heads x kv_sub
     int kv_sub;    // query-head groups per physical kv head (group = kv_sub x G)
     int kv_cap;
-    int chunks;  // workgroups per kv head group
+    int chunks;  // chunks of the window list per kv head group
+    int split;   // 0: equal chunks; else chunk pairs, the first taking split/256 (ChunkMap)
     float scale_log2;
+};
+
+// Window ranges of the chunks of one kv head group (W windows): chunk c covers
+// [lo(c), lo(c + 1)). split == 0: P equal chunks, lo(c) = c W / P. split > 0 (P
+// even): chunks 2j and 2j + 1 share the j-th of P / 2 equal ranges, the first
+// taking split / 256 of it (the fused cascade kernel's two roles on one CU).
+// x / d for x >= 0, d > 0: 32-bit division (a dozen instructions) whenever x
+// fits, the 64-bit routine (several times longer) only beyond.
+__device__ __forceinline__ int64_t div_nonneg(int64_t x, int64_t d) {
+    if (((uint64_t)x >> 32) == 0 && ((uint64_t)d >> 32) == 0) return (int64_t)((uint32_t)x / (uint32_t)d);
+    return x / d;
+}
+
+struct ChunkMap {
+    int64_t W;
+    int P;
+    int split;
+    __device__ __forceinline__ int64_t lo(int c) const {
+        if (split == 0) return div_nonneg((int64_t)c * W, P);
+        const int h = P >> 1, j = c >> 1;
+        const int64_t a = div_nonneg((int64_t)j * W, h);
+        if ((c & 1) == 0) return a;
+        return a + (((div_nonneg((int64_t)(j + 1) * W, h) - a) * split) >> 8);
+    }
+    // the chunk that owns window p < W
+    __device__ __forceinline__ int owner(int64_t p) const {
+        if (split == 0) return (int)div_nonneg((p + 1) * P - 1, W);
+        const int j = (int)div_nonneg((p + 1) * (P >> 1) - 1, W);
+        return 2 * j + (p >= lo(2 * j + 1) ? 1 : 0);
+    }
+    __device__ __forceinline__ bool empty(int c) const { return lo(c) == lo(c + 1); }
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -244,16 +280,35 @@ __device__ __forceinline__ int seq_of_window(const CK_LDS int *cw, int batch, in
 // The stream body on NW waves (thread tid of the group's NW * 64) as workgroup lb
 // of a grid of a.kv_heads * a.chunks, with the group's LDS at smem and its own
 // barrier. Windows hold 8 NW tokens.
-template <int G, int NW, int D, class Bar>
+//
+// Two lane layouts for V and the value accumulators:
+// * TOK = false (dims-major): lane (hf, dd) holds dims 4dd .. 4dd+3 of 4 tokens;
+//   p reaches it through a per-wave LDS row and q is read from LDS per window.
+//   4 accumulators per head: fits 128 registers.
+// * TOK = true (token-major, G <= 4): V uses K's layout, lane (t, c) holds dims
+//   8c .. 8c+7 and 64+8c .. 64+8c+7 of token t, so the lane already owns the p of
+//   its token; q sits in registers for the whole segment. The window loop then
+//   makes no LDS access besides one table read, and its arithmetic never waits
+//   on the LDS pipe (which the fused kernel's stage-1 waves keep busy). 16
+//   accumulators per head, summed over the 8 token slots when a segment closes.
+//
+// Two bodies on one CU may share one scan: the body given scan_src (the other
+// body's LDS) skips its own, waits until scan_flag is set and reads the other's
+// lengths and window prefix sums; the body given only scan_flag sets it once its
+// scan is complete.
+template <int G, int NW, int D, bool TOK, class Bar>
 __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS char *smem, int lb, int tid,
-                                                   const Bar &bar) {
+                                                   const Bar &bar, CK_LDS int *scan_flag = nullptr,
+                                                   const CK_LDS char *scan_src = nullptr) {
+    static_assert(!TOK || G <= 4, "token-major layout: at most 4 query heads per group");
     constexpr int NB = D + 1;  // register ring slots: D windows in flight + the one in use
+    constexpr int kAcc = TOK ? 16 : 4;  // value accumulators per head and lane
     constexpr int kThr = NW * 64;
     constexpr int kWin = 8 * NW;         // tokens per window
     constexpr int kWpp = kPage / kWin;   // windows per page
     using L = SfxLds<G, NW>;
-    CK_LDS int *cw = (CK_LDS int *)(smem + L::kCw);
-    CK_LDS int *len = (CK_LDS int *)(smem + L::kLen);
+    CK_LDS int *cw = (CK_LDS int *)((scan_src ? scan_src : smem) + L::kCw);
+    CK_LDS int *len = (CK_LDS int *)((scan_src ? scan_src : smem) + L::kLen);
     CK_LDS int *wtot = (CK_LDS int *)(smem + L::kWtot);
     CK_LDS i32x2 *tab = (CK_LDS i32x2 *)(smem + L::kTab);
     CK_LDS char *qs = smem + L::kQs;
@@ -279,42 +334,50 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     }
 
     // ---- lengths and window prefix sums (kPer sequences per thread, block scan) ----
-    constexpr int kPer = kMaxBatch / kThr;
-    int lv[kPer];
-    int local = 0;
+    if (scan_src == nullptr) {
+        constexpr int kPer = kMaxBatch / kThr;
+        int lv[kPer];
+        int local = 0;
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const int i = kPer * tid + j;
-        const int ln = i < a.batch ? (int)clamp_len(a, a.kv_seqlens[i]) : 0;
-        if (i < a.batch) len[i] = ln;
-        lv[j] = (ln + kWin - 1) / kWin;
-        local += lv[j];
-    }
-    int x = local;
+        for (int j = 0; j < kPer; ++j) {
+            const int i = kPer * tid + j;
+            const int ln = i < a.batch ? (int)clamp_len(a, a.kv_seqlens[i]) : 0;
+            if (i < a.batch) len[i] = ln;
+            lv[j] = (ln + kWin - 1) / kWin;
+            local += lv[j];
+        }
+        int x = local;
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(x, off);
-        if (lane >= off) x += y;
-    }
-    if (lane == 63) wtot[wid] = x;
-    bar.sync();
-    int wave_off = 0;
-    for (int ww = 0; ww < wid; ++ww) wave_off += wtot[ww];
-    int run = wave_off + x - local;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(x, off);
+            if (lane >= off) x += y;
+        }
+        if (lane == 63) wtot[wid] = x;
+        bar.sync();
+        int wave_off = 0;
+        for (int ww = 0; ww < wid; ++ww) wave_off += wtot[ww];
+        int run = wave_off + x - local;
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const int i = kPer * tid + j;
-        run += lv[j];
-        if (i < a.batch) cw[i + 1] = run;
+        for (int j = 0; j < kPer; ++j) {
+            const int i = kPer * tid + j;
+            run += lv[j];
+            if (i < a.batch) cw[i + 1] = run;
+        }
+        if (tid == 0) cw[0] = 0;
+        bar.sync();
+        if (lb == 0)
+            for (int i = tid; i <= a.batch; i += kThr) a.cw_out[i] = cw[i];
+        if (scan_flag != nullptr && tid == 0) *(volatile CK_LDS int *)scan_flag = 1;  // after the barrier above
+    } else {
+        // the other body's scan (bounded: it always completes, long before this bound)
+        for (int spin = 0; *(volatile CK_LDS int *)scan_flag == 0 && spin < (1 << 22); ++spin)
+            __builtin_amdgcn_s_sleep(1);
     }
-    if (tid == 0) cw[0] = 0;
-    bar.sync();
-    if (lb == 0)
-        for (int i = tid; i <= a.batch; i += kThr) a.cw_out[i] = cw[i];
 
     const int W = cw[a.batch];
-    const int w0 = (int)((int64_t)chunk * W / a.chunks);
-    const int w1 = (int)((int64_t)(chunk + 1) * W / a.chunks);
+    const ChunkMap cm{W, a.chunks, a.split};
+    const int w0 = (int)cm.lo(chunk);
+    const int w1 = (int)cm.lo(chunk + 1);
     if (w0 >= w1) return;  // uniform over the workgroup
 
     // ---- q rows: the s-th segment of a phase in slot s ------------------------------
@@ -337,24 +400,27 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     // ---- per-lane constants ------------------------------------------------------------
     const int64_t tokb = a.tok_stride * 2;                      // bytes between token rows
     const uint32_t koff = (uint32_t)((8 * wid + t) * tokb + c * 16);   // K byte offset in a window
-    const uint32_t voff = (uint32_t)((8 * wid + hf) * tokb + dd * 8);  // V byte offset of token hf
+    const uint32_t voff = TOK ? koff : (uint32_t)((8 * wid + hf) * tokb + dd * 8);  // V byte offset
     const uint32_t win_bytes = (uint32_t)(kWin * tokb);          // a window's buffer range
     const char *kbase = reinterpret_cast<const char *>(a.k) + (int64_t)gk * a.head_off * 2;
     const char *vbase = reinterpret_cast<const char *>(a.v) + (int64_t)gk * a.head_off * 2;
     const int64_t pgb = a.page_stride * 2;
 
-    float m[G], l[G], acc[G][4];
+    float m[G], l[G], acc[G][kAcc];
     int nclose = 0;  // segments closed so far (exchange ring position)
     int qslot = 0;   // segment of the current phase
     u32x4 kbuf[NB][2];
-    u32x2 vbuf[NB][4];
+    using VSlot = std::conditional_t<TOK, u32x4[2], u32x2[4]>;
+    VSlot vbuf[NB];
+    u32x4 qr[TOK ? G : 1][2];  // token-major: this lane's 16 q dims of each head
+    int eyr[NB];               // token-major: packed table fields of the window in each slot
     constexpr int kPwRow = (G + 3) / 4 * 4;  // floats per token in this wave's p rows
     static_assert(kPwRow <= 8, "p row");
     CK_LDS float *pw = (CK_LDS float *)(smem + L::kPw) + wid * 64;
 
     // K/V loads of the window with table entry e (e[0] < 0: invalid page; a dummy
     // entry past the phase end has e[1] = 0, no valid tokens) into one ring slot
-    auto issue = [&](i32x2 e, u32x4 &k0, u32x4 &k1, u32x2 *vv) __attribute__((always_inline)) {
+    auto issue = [&](i32x2 e, u32x4 &k0, u32x4 &k1, VSlot &vv) __attribute__((always_inline)) {
         const int page = __builtin_amdgcn_readfirstlane(e[0]);
         const int ey = __builtin_amdgcn_readfirstlane(e[1]);
         const int64_t off = (int64_t)(page < 0 ? 0 : page) * pgb + (int64_t)(tab_sub(ey) * kWin) * tokb;
@@ -367,16 +433,159 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         const uint32_t o = t < t1 ? koff : kOob;
         k0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)o, 0, 0));
         k1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)(o + 128), 0, 0));
+        if constexpr (TOK) {
+            vv[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, (int)o, 0, 0));
+            vv[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, (int)(o + 128), 0, 0));
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t ov = 2 * j + hf < t1 ? voff + (uint32_t)(2 * j * tokb) : kOob;
-            vv[j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)ov, 0, 0));
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t ov = 2 * j + hf < t1 ? voff + (uint32_t)(2 * j * tokb) : kOob;
+                vv[j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)ov, 0, 0));
+            }
         }
+    };
+
+    // Closes segment b (sequence b's windows in this range): folds the lanes' partial
+    // sums, hands the wave's (O, m, l) to the exchange ring, and the last wave in
+    // merges the NW partials and writes the result.
+    auto close_seg = [&](int b) __attribute__((always_inline)) {
+        // token-major with 4 heads: a reduce-scatter over the 8 token slots. The
+        // 64 accumulators of a lane, flat index f = 16 h + e, are halved twice by
+        // lane swaps (the half-wave bit keeps f's bit 5, the 16-lane-row bit f's
+        // bit 4) and the last slot bit is summed by DPP: lane (s5, s4, s3, c) ends
+        // with head 2 s5 + s4, all 16 of its dims, in 112 instructions instead of
+        // 320 for summing every accumulator over all 8 slots.
+        float f2[16];
+#pragma unroll
+        for (int h = 0; h < G; ++h) l[h] = sum_slots(l[h]);
+        if constexpr (TOK && G == 4) {
+            float f1[32];
+#pragma unroll
+            for (int j = 0; j < 32; ++j) {
+                const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[j >> 4][j & 15]),
+                                                                __float_as_uint(acc[(j + 32) >> 4][j & 15]), false,
+                                                                false);
+                f1[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const auto r =
+                    __builtin_amdgcn_permlane16_swap(__float_as_uint(f1[j]), __float_as_uint(f1[j + 16]), false, false);
+                f2[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+            }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) f2[e] += CK_DPP(f2[e], 0x128);  // row_ror:8: lane ^ 8
+        } else {
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+#pragma unroll
+                for (int e = 0; e < kAcc; ++e)  // dims-major: the two half-waves; token-major: the 8 token slots
+                    acc[h][e] = TOK ? sum_slots(acc[h][e]) : sum_xor32(acc[h][e]);
+            }
+        }
+        const int r = nclose % R;
+        const int want = nclose / R;  // merges the slot has seen before this segment
+        // the slot's previous segment must be merged (bounded: a wait that never
+        // ended would mean a broken invariant, and results then are wrong, not hung)
+        for (int spin = 0; *(volatile CK_LDS int *)(xgen + r) != want && spin < (1 << 22); ++spin)
+            __builtin_amdgcn_s_sleep(1);
+        CK_LDS float *xo_r = xo + r * NW * G * kD;
+        CK_LDS float *xml_r = xml + r * NW * G * 2;
+        if constexpr (TOK && G == 4) {
+            if ((lane & 8) == 0) {
+                CK_LDS float *dst = xo_r + (wid * G + (lane >> 4)) * kD + 8 * c;
+                *reinterpret_cast<CK_LDS f32x4 *>(dst) = f32x4{f2[0], f2[1], f2[2], f2[3]};
+                *reinterpret_cast<CK_LDS f32x4 *>(dst + 4) = f32x4{f2[4], f2[5], f2[6], f2[7]};
+                *reinterpret_cast<CK_LDS f32x4 *>(dst + 64) = f32x4{f2[8], f2[9], f2[10], f2[11]};
+                *reinterpret_cast<CK_LDS f32x4 *>(dst + 68) = f32x4{f2[12], f2[13], f2[14], f2[15]};
+            }
+        } else if constexpr (TOK) {
+            // every token slot holds the sums: slot h writes head h
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                if (t == h) {
+                    CK_LDS float *dst = xo_r + (wid * G + h) * kD + 8 * c;
+                    *reinterpret_cast<CK_LDS f32x4 *>(dst) = f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+                    *reinterpret_cast<CK_LDS f32x4 *>(dst + 4) = f32x4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+                    *reinterpret_cast<CK_LDS f32x4 *>(dst + 64) =
+                        f32x4{acc[h][8], acc[h][9], acc[h][10], acc[h][11]};
+                    *reinterpret_cast<CK_LDS f32x4 *>(dst + 68) =
+                        f32x4{acc[h][12], acc[h][13], acc[h][14], acc[h][15]};
+                }
+            }
+        } else if (hf == 0) {
+#pragma unroll
+            for (int h = 0; h < G; ++h)
+                *reinterpret_cast<CK_LDS f32x4 *>(xo_r + (wid * G + h) * kD + 4 * dd) =
+                    f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                xml_r[(wid * G + h) * 2] = m[h];
+                xml_r[(wid * G + h) * 2 + 1] = l[h];
+            }
+        }
+        // a wave's LDS operations complete in order: its rows are in before it counts itself
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        int old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(xcnt + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        old = __builtin_amdgcn_readfirstlane(old);
+        if (old == NW - 1) {
+            // the last wave in: merge the 8 partials of every query head
+            asm volatile("" ::: "memory");
+#pragma unroll 1
+            for (int u0 = 0; u0 < 32 * G; u0 += 64) {
+                const int u = u0 + lane;
+                if (u < 32 * G) {
+                    const int h = u >> 5, d4 = u & 31;
+                    float mx = -INFINITY;
+#pragma unroll
+                    for (int ww = 0; ww < NW; ++ww) mx = fmaxf(mx, xml_r[(ww * G + h) * 2]);
+                    const float mz = mx == -INFINITY ? 0.f : mx;
+                    float lt = 0.f;
+                    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ww = 0; ww < NW; ++ww) {
+                        const float f = exp2_fast(xml_r[(ww * G + h) * 2] - mz);
+                        lt = fmaf(xml_r[(ww * G + h) * 2 + 1], f, lt);
+                        const f32x4 xa =
+                            *reinterpret_cast<const CK_LDS f32x4 *>(xo_r + (ww * G + h) * kD + 4 * d4);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) o[e] = fmaf(xa[e], f, o[e]);
+                    }
+                    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+                    const float lse_v = lt > 0.f ? (mx + __log2f(lt)) * kLn2 : -INFINITY;
+                    const bool head_part = cw[b] < w0;
+                    const bool tail_part = cw[b + 1] > w1;
+                    if (!head_part && !tail_part) {
+                        const int64_t row = (int64_t)b * a.num_heads + g * G + h;
+                        *reinterpret_cast<uint2 *>(a.out + row * kD + 4 * d4) = make_uint2(
+                            pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv));
+                        if (d4 == 0) a.lse[row] = lse_v;
+                    } else {
+                        const int64_t pidx =
+                            (((int64_t)g * a.chunks + chunk) * 2 + (head_part ? 0 : 1)) * G + h;
+                        *reinterpret_cast<float4 *>(a.part_o + pidx * kD + 4 * d4) =
+                            make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+                        if (d4 == 0) a.part_lse[pidx] = lse_v;
+                    }
+                }
+            }
+            // free the slot: reset its count, then publish the merge
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lane == 0) xcnt[r] = 0;
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lane == 0) xgen[r] = want + 1;
+        }
+        ++nclose;
+        ++qslot;
     };
 
     // One window of a phase: issue window n + D into the slot freed last step,
     // compute window n from slot J = n % NB, close its segment if it ends here.
     auto step = [&](auto jc, int n, int np) __attribute__((always_inline)) {
+      if constexpr (!TOK) {
         constexpr int J = decltype(jc)::value;
         constexpr int JI = (J + D) % NB;  // slot of window n + D (freed by window n - 1)
         const int ni = n + D;
@@ -458,90 +667,86 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             }
         }
 
-        if (tab_last(ey)) {
-            // ---- close the segment ---------------------------------------------------
+        if (tab_last(ey)) close_seg(b);
+      }
+    };
+
+    // Token-major window step: the table entry of the window to issue was read
+    // one step ahead and the packed fields of the window computed here travel in
+    // the ring with its data, so the step's only LDS access (the entry for the
+    // next step) is off its critical path.
+    i32x2 enext = i32x2{-1, 0};
+    auto step_tok = [&](auto jc, int n, int np) __attribute__((always_inline)) {
+      if constexpr (TOK) {
+        constexpr int J = decltype(jc)::value;
+        constexpr int JI = (J + D) % NB;
+        const i32x2 ei = enext;
+        issue(ei, kbuf[JI][0], kbuf[JI][1], vbuf[JI]);
+        const int ey = eyr[J];
+        eyr[JI] = __builtin_amdgcn_readfirstlane(ei[1]);
+        enext = n + D + 1 < np ? tab[n + D + 1] : i32x2{-1, 0};
+
+        const int b = tab_b(ey);
+        const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
+        if (tab_first(ey)) {
+            const CK_LDS char *qrow = qs + qslot * G * (kD * 2) + c * 16;
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                l[h] = sum_slots(l[h]);
+                qr[h][0] = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2));
+                qr[h][1] = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2) + 128);
+                m[h] = -INFINITY;
+                l[h] = 0.f;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[h][e] = sum_xor32(acc[h][e]);  // the two half-waves
+                for (int e = 0; e < kAcc; ++e) acc[h][e] = 0.f;
             }
-            const int r = nclose % R;
-            const int want = nclose / R;  // merges the slot has seen before this segment
-            // the slot's previous segment must be merged (bounded: a wait that never
-            // ended would mean a broken invariant, and results then are wrong, not hung)
-            for (int spin = 0; *(volatile CK_LDS int *)(xgen + r) != want && spin < (1 << 22); ++spin)
-                __builtin_amdgcn_s_sleep(1);
-            CK_LDS float *xo_r = xo + r * NW * G * kD;
-            CK_LDS float *xml_r = xml + r * NW * G * 2;
-            if (hf == 0) {
+        }
+        if (t1 > 0) {
+            const u32x4 k0 = kbuf[J][0], k1 = kbuf[J][1];
+            float s[G];  // scores, then p in place
+            bool trig = false;
 #pragma unroll
-                for (int h = 0; h < G; ++h)
-                    *reinterpret_cast<CK_LDS f32x4 *>(xo_r + (wid * G + h) * kD + 4 * dd) =
-                        f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+            for (int h = 0; h < G; ++h) s[h] = sum8(dot16(k0, k1, qr[h][0], qr[h][1])) * a.scale_log2;
+            if (t1 < 8) {
+#pragma unroll
+                for (int h = 0; h < G; ++h) s[h] = t < t1 ? s[h] : -INFINITY;
             }
-            if (lane == 0) {
+#pragma unroll
+            for (int h = 0; h < G; ++h) trig |= s[h] > m[h] + kTau;  // m = -inf: always
+            if (__builtin_amdgcn_ballot_w64(trig)) {
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
-                    xml_r[(wid * G + h) * 2] = m[h];
-                    xml_r[(wid * G + h) * 2 + 1] = l[h];
-                }
-            }
-            // a wave's LDS operations complete in order: its rows are in before it counts itself
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            int old = 0;
-            if (lane == 0) old = __hip_atomic_fetch_add(xcnt + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            old = __builtin_amdgcn_readfirstlane(old);
-            if (old == NW - 1) {
-                // the last wave in: merge the 8 partials of every query head
-                asm volatile("" ::: "memory");
-#pragma unroll 1
-                for (int u0 = 0; u0 < 32 * G; u0 += 64) {
-                    const int u = u0 + lane;
-                    if (u < 32 * G) {
-                        const int h = u >> 5, d4 = u & 31;
-                        float mx = -INFINITY;
+                    const float m_new = fmaxf(m[h], max_slots(s[h]));
+                    if (m_new > m[h]) {
+                        const float f = exp2_fast(m[h] - m_new);  // 0 from -inf
 #pragma unroll
-                        for (int ww = 0; ww < NW; ++ww) mx = fmaxf(mx, xml_r[(ww * G + h) * 2]);
-                        const float mz = mx == -INFINITY ? 0.f : mx;
-                        float lt = 0.f;
-                        f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                        for (int ww = 0; ww < NW; ++ww) {
-                            const float f = exp2_fast(xml_r[(ww * G + h) * 2] - mz);
-                            lt = fmaf(xml_r[(ww * G + h) * 2 + 1], f, lt);
-                            const f32x4 xa =
-                                *reinterpret_cast<const CK_LDS f32x4 *>(xo_r + (ww * G + h) * kD + 4 * d4);
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) o[e] = fmaf(xa[e], f, o[e]);
-                        }
-                        const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-                        const float lse_v = lt > 0.f ? (mx + __log2f(lt)) * kLn2 : -INFINITY;
-                        const bool head_part = cw[b] < w0;
-                        const bool tail_part = cw[b + 1] > w1;
-                        if (!head_part && !tail_part) {
-                            const int64_t row = (int64_t)b * a.num_heads + g * G + h;
-                            *reinterpret_cast<uint2 *>(a.out + row * kD + 4 * d4) = make_uint2(
-                                pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv));
-                            if (d4 == 0) a.lse[row] = lse_v;
-                        } else {
-                            const int64_t pidx =
-                                (((int64_t)g * a.chunks + chunk) * 2 + (head_part ? 0 : 1)) * G + h;
-                            *reinterpret_cast<float4 *>(a.part_o + pidx * kD + 4 * d4) =
-                                make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
-                            if (d4 == 0) a.part_lse[pidx] = lse_v;
-                        }
+                        for (int e = 0; e < kAcc; ++e) acc[h][e] *= f;
+                        l[h] *= f;
+                        m[h] = m_new;
                     }
                 }
-                // free the slot: reset its count, then publish the merge
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                if (lane == 0) xcnt[r] = 0;
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                if (lane == 0) xgen[r] = want + 1;
             }
-            ++nclose;
-            ++qslot;
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                s[h] = exp2_fast(s[h] - (m[h] == -INFINITY ? 0.f : m[h]));  // 0 for masked tokens
+                l[h] += s[h];
+            }
+            const u32x4 v0 = vbuf[J][0], v1 = vbuf[J][1];
+            float vf[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                vf[2 * i] = bf16_lo(v0[i]);
+                vf[2 * i + 1] = bf16_hi(v0[i]);
+                vf[8 + 2 * i] = bf16_lo(v1[i]);
+                vf[9 + 2 * i] = bf16_hi(v1[i]);
+            }
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[h][e] = fmaf(s[h], vf[e], acc[h][e]);
+            }
         }
+        if (tab_last(ey)) close_seg(b);
+      }
     };
 
     // ---- phases of up to kTable windows and kQSlots segments: table and q rows,
@@ -580,18 +785,26 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         for (int j = 0; j < D; ++j) {
             const i32x2 e = j < np ? tab[j] : i32x2{-1, 0};
             issue(e, kbuf[j][0], kbuf[j][1], vbuf[j]);
+            if constexpr (TOK) eyr[j] = __builtin_amdgcn_readfirstlane(e[1]);
         }
+        if constexpr (TOK) enext = D < np ? tab[D] : i32x2{-1, 0};
         // full rounds of NB steps, then the rest: the ring slot of every step is a
         // compile-time constant and no step leaves the loop early, so the
         // compiler's vmcnt bookkeeping sees one path around the back edge
         int n = 0;
         for (int it = np / NB; it > 0; --it) {
-            static_for<NB>([&](auto jc) __attribute__((always_inline)) { step(jc, n + decltype(jc)::value, np); });
+            static_for<NB>([&](auto jc) __attribute__((always_inline)) {
+                if constexpr (TOK) step_tok(jc, n + decltype(jc)::value, np);
+                else step(jc, n + decltype(jc)::value, np);
+            });
             n += NB;
         }
         const int rem = np - n;
         static_for<NB>([&](auto jc) __attribute__((always_inline)) {
-            if (decltype(jc)::value < rem) step(jc, n + decltype(jc)::value, np);
+            if (decltype(jc)::value < rem) {
+                if constexpr (TOK) step_tok(jc, n + decltype(jc)::value, np);
+                else step(jc, n + decltype(jc)::value, np);
+            }
         });
         p0 = p1;
     }
@@ -603,17 +816,12 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
 template <int G>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void suffix_stream_kernel(SuffixArgs a) {
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-    suffix_stream_body<G, kWaves, kDepth>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
+    suffix_stream_body<G, kWaves, kDepth, false>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
 }
 template <int G>
 __global__ __launch_bounds__(kThreads) void suffix_stream_wide_kernel(SuffixArgs a) {
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-    suffix_stream_body<G, kWaves, kDepth>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
-}
-
-// Chunk that owns window p: chunk c covers windows [c*W/P, (c+1)*W/P).
-__device__ __forceinline__ int owner_chunk(int64_t p, int64_t W, int P) {
-    return (int)(((p + 1) * P - 1) / W);
+    suffix_stream_body<G, kWaves, kDepth, false>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
 }
 
 // Folds the partials of one query head of a sequence cut by chunk boundaries
@@ -623,12 +831,12 @@ __device__ __forceinline__ int owner_chunk(int64_t p, int64_t W, int P) {
 // costs one memory round trip; longer runs continue in a loop. The arithmetic
 // (max over all, then a weighted sum in chunk order) does not depend on kPre.
 template <int G>
-__device__ __forceinline__ void fold_cut(const float *part_o, const float *part_lse, int g, int chunks, int hq,
-                                         int d4, int ca, int cb, int64_t W, float4 &o_out, float &lse_out) {
+__device__ __forceinline__ void fold_cut(const float *part_o, const float *part_lse, int g, const ChunkMap &cm,
+                                         int hq, int d4, int ca, int cb, float4 &o_out, float &lse_out) {
     constexpr int kPre = 4;
-    auto pidx = [&](int ch, int sl) { return (((int64_t)g * chunks + ch) * 2 + sl) * G + hq; };
-    // a chunk with no windows (W < P) wrote nothing
-    auto empty_chunk = [&](int ch) { return (int64_t)ch * W / chunks == (int64_t)(ch + 1) * W / chunks; };
+    auto pidx = [&](int ch, int sl) { return (((int64_t)g * cm.P + ch) * 2 + sl) * G + hq; };
+    // a chunk with no windows wrote nothing
+    auto empty_chunk = [&](int ch) { return cm.empty(ch); };
     float pl[kPre];
     float4 po[kPre];
     bool ok[kPre];
@@ -686,12 +894,13 @@ __global__ __launch_bounds__(kMaxGroup * 32) void suffix_fixup_kernel(SuffixArgs
         if (d4 == 0) a.lse[row] = -INFINITY;
         return;
     }
-    const int ca = owner_chunk(beg, W, a.chunks);
-    const int cb = owner_chunk(end - 1, W, a.chunks);
+    const ChunkMap cm{W, a.chunks, a.split};
+    const int ca = cm.owner(beg);
+    const int cb = cm.owner(end - 1);
     if (ca == cb) return;  // written by the stream kernel
     float4 o;
     float l;
-    fold_cut<G>(a.part_o, a.part_lse, g, a.chunks, hq, d4, ca, cb, W, o, l);
+    fold_cut<G>(a.part_o, a.part_lse, g, cm, hq, d4, ca, cb, o, l);
     *reinterpret_cast<uint2 *>(a.out + row * kD + 4 * d4) =
         make_uint2(pack_bf16x2(o.x, o.y), pack_bf16x2(o.z, o.w));
     if (d4 == 0) a.lse[row] = l;
@@ -722,6 +931,7 @@ struct EpilogueArgs {
     int num_heads;
     int kv_heads;  // kv head groups, as in SuffixArgs
     int chunks;
+    int split;
 };
 
 template <int G>
@@ -757,15 +967,16 @@ __global__ __launch_bounds__(kMaxGroup * 32) void cascade_epilogue_kernel(Epilog
     float l2 = -INFINITY;
     float4 o2 = make_float4(0.f, 0.f, 0.f, 0.f);
     if (end > beg) {
-        const int ca = owner_chunk(beg, W, e.chunks);
-        const int cb = owner_chunk(end - 1, W, e.chunks);
+        const ChunkMap cm{W, e.chunks, e.split};
+        const int ca = cm.owner(beg);
+        const int cb = cm.owner(end - 1);
         if (ca == cb) {
             const int64_t r2 = (int64_t)bl * e.num_heads + h;
             const uint2 w = *reinterpret_cast<const uint2 *>(e.o2 + r2 * kD + 4 * d4);
             o2 = make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
             l2 = e.lse2[r2];
         } else {
-            fold_cut<G>(e.part_o, e.part_lse, g, e.chunks, hq, d4, ca, cb, W, o2, l2);
+            fold_cut<G>(e.part_o, e.part_lse, g, cm, hq, d4, ca, cb, o2, l2);
         }
     }
 
@@ -838,31 +1049,41 @@ __global__ __launch_bounds__(kMaxGroup * 32) void cascade_epilogue_kernel(Epilog
 }
 
 // Fused cascade kernel: workgroup i runs stage-1 unit i on waves 0-3 (the
-// 128-row body with a 3-slot ring) and suffix chunk i on waves 4-7 (the stream
-// body on 4 waves, 32-token windows), side by side on one CU: each SIMD holds
-// one MFMA wave and one streaming wave, which fill each other's stalls, and the
-// prefix pages and the suffix pages stream at the same time. Each role has its
-// own LDS region and its own barrier; neither waits for the other.
+// 128-row body with a 3-slot ring) and suffix chunk 2j on waves 4-7 (the stream
+// body on 4 waves, 32-token windows) side by side on one CU: each SIMD holds one
+// MFMA wave and one streaming wave, which fill each other's stalls, and the
+// prefix pages and the suffix pages stream at the same time. When its stage-1
+// unit is done, waves 0-3 stream suffix chunk 2j + 1, the last (256 - split) /
+// 256 of the workgroup's windows, in the LDS the stage-1 tiles used: the two
+// roles end together instead of the stage-1 waves idling while the suffix
+// waves finish. Each role has its own LDS region and barrier; neither waits
+// for the other.
 constexpr int kFusedS1Lds = s1::wide_lds_bytes<3>();
 template <int G>
-constexpr int fused_lds_bytes() { return kFusedS1Lds + SfxLds<G, 4>::kBytes + 16; }
+constexpr int fused_lds_bytes() { return kFusedS1Lds + SfxLds<G, 4>::kBytes + 32; }
 static_assert(fused_lds_bytes<kMaxGroup>() <= 160 * 1024, "one fused workgroup per CU");
+static_assert(SfxLds<kMaxGroup, 4>::kBytes <= kFusedS1Lds, "the stage-1 waves' stream body fits the tile ring");
 
 template <int G>
 __global__ __launch_bounds__(512) void cascade_fused_kernel(s1::Stage1Args s1a, int n1, SuffixArgs sa, int n2) {
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
     CK_LDS char *smem = (CK_LDS char *)smem_raw;
     CK_LDS int *bars = (CK_LDS int *)(smem + kFusedS1Lds + SfxLds<G, 4>::kBytes);
-    if (threadIdx.x < 4) bars[threadIdx.x] = 0;
+    if (threadIdx.x < 5) bars[threadIdx.x] = 0;  // two role barriers, the scan flag
     __syncthreads();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (wave < 4) {
-        if ((int)blockIdx.x < n1)
-            s1::stage1_wide_body<4, 3>(s1a, smem, blockIdx.x, n1, threadIdx.x, GroupBarrier{bars, bars + 1, 4});
-    } else {
-        if ((int)blockIdx.x < n2)
-            suffix_stream_body<G, 4, kFusedDepth>(sa, smem + kFusedS1Lds, blockIdx.x, threadIdx.x - 256,
-                                     GroupBarrier{bars + 2, bars + 3, 4});
+    const int role = wave < 4 ? 1 : 0;  // 1: stage-1 waves (suffix chunk 2j + 1 afterwards)
+    const GroupBarrier bar{bars + 2 * (1 - role), bars + 2 * (1 - role) + 1, 4};
+    if (role == 1 && (int)blockIdx.x < n1) {
+        s1::stage1_wide_body<4, 3>(s1a, smem, blockIdx.x, n1, threadIdx.x, bar);
+        bar.sync();  // every stage-1 wave is done with the tile ring
+    }
+    if ((int)blockIdx.x < n2) {
+        const int g = (int)blockIdx.x % sa.kv_heads, j = (int)blockIdx.x / sa.kv_heads;
+        // the streaming waves scan the lengths; the stage-1 waves reuse that scan
+        suffix_stream_body<G, 4, (G <= 4 ? kFusedTokDepth : kFusedDepth), (G <= 4)>(
+            sa, smem + (role ? 0 : kFusedS1Lds), (2 * j + role) * sa.kv_heads + g, threadIdx.x & 255, bar, bars + 4,
+            role ? smem + kFusedS1Lds : nullptr);
     }
 }
 
@@ -879,7 +1100,7 @@ int launch_fused(const s1::Stage1Args &s1a, int64_t n1, const SuffixArgs &a, con
     constexpr int kLds = fused_lds_bytes<G>();
     int rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&cascade_fused_kernel<G>), kLds, lds_set);
     if (rc != CK_OK) return rc;
-    const int64_t n2 = (int64_t)a.kv_heads * a.chunks;
+    const int64_t n2 = (int64_t)a.kv_heads * (a.chunks / 2);  // chunk pairs (a.split > 0)
     const int64_t grid = n1 > n2 ? n1 : n2;
     hipLaunchKernelGGL(cascade_fused_kernel<G>, dim3((unsigned)grid), dim3(512), kLds, st, s1a, (int)n1, a, (int)n2);
     hipError_t e = hipGetLastError();
@@ -956,7 +1177,7 @@ int64_t suffix_default_chunks(int64_t num_heads, int64_t kv_heads) {
 int64_t suffix_fused_chunks(int64_t num_heads, int64_t kv_heads) {
     const int64_t groups = kv_heads * suffix_sub_groups(num_heads, kv_heads);
     const int64_t p = 256 / groups;
-    return p > 0 ? p : 1;
+    return 2 * (p > 0 ? p : 1);  // a pair of chunks per fused workgroup
 }
 
 int64_t suffix_group_ws_bytes(int64_t nb, int64_t num_heads, int64_t kv_heads, int64_t chunks) {
@@ -994,6 +1215,7 @@ int suffix_launch_group(const void *q, const void *k, const void *v, const int32
     a.kv_sub = (int)sub;
     a.kv_cap = (int)kv_cap;
     a.chunks = (int)chunks;
+    a.split = fused && cascade ? kFusedSplit : 0;
     a.scale_log2 = scale * kLog2e;
     EpilogueArgs e;
     if (cascade) {
@@ -1010,6 +1232,7 @@ int suffix_launch_group(const void *q, const void *k, const void *v, const int32
         e.num_heads = (int)num_heads;
         e.kv_heads = a.kv_heads;
         e.chunks = (int)chunks;
+        e.split = a.split;
     }
     if (fused && cascade) {
         switch (G) {
