@@ -110,7 +110,7 @@ constexpr int kRsrcFlags = 0x00020000;  // buffer descriptor word 3 for gfx9 raw
 // kernel, whose 4 streaming waves per CU carry the CU's whole share.
 constexpr int kDepth = 1;
 constexpr int kFusedDepth = 4;
-constexpr int kFusedTokDepth = 3;  // token-major: 16 registers per window and lane
+constexpr int kFusedTokDepth = 2;  // token-major: 16 registers per window and lane
 // Share of each fused workgroup's suffix windows that its streaming waves take
 // (in 1/256); the stage-1 waves take the rest after their stage-1 unit.
 constexpr int kFusedSplit = 192;
@@ -671,66 +671,21 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
       }
     };
 
-    // Token-major window step: the table entry of the window to issue was read
-    // one step ahead and the packed fields of the window computed here travel in
-    // the ring with its data, so the step's only LDS access (the entry for the
-    // next step) is off its critical path.
+    // Token-major window step, pipelined by one window: step n issues window
+    // n + D, computes the scores of window n and the values of window n - 1 (its p
+    // and V rows kept from the step before) -- two independent chains in one basic
+    // block, so each fills the other's latencies -- then closes window n - 1's
+    // segment if it ends there and finishes window n's softmax. The table entry of
+    // the window to issue was read one step ahead and the packed fields of each
+    // window travel in the ring with its data, so the step's only LDS access is
+    // off its critical path.
     i32x2 enext = i32x2{-1, 0};
-    auto step_tok = [&](auto jc, int n, int np) __attribute__((always_inline)) {
-      if constexpr (TOK) {
-        constexpr int J = decltype(jc)::value;
-        constexpr int JI = (J + D) % NB;
-        const i32x2 ei = enext;
-        issue(ei, kbuf[JI][0], kbuf[JI][1], vbuf[JI]);
-        const int ey = eyr[J];
-        eyr[JI] = __builtin_amdgcn_readfirstlane(ei[1]);
-        enext = n + D + 1 < np ? tab[n + D + 1] : i32x2{-1, 0};
-
-        const int b = tab_b(ey);
-        const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
-        if (tab_first(ey)) {
-            const CK_LDS char *qrow = qs + qslot * G * (kD * 2) + c * 16;
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                qr[h][0] = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2));
-                qr[h][1] = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2) + 128);
-                m[h] = -INFINITY;
-                l[h] = 0.f;
-#pragma unroll
-                for (int e = 0; e < kAcc; ++e) acc[h][e] = 0.f;
-            }
-        }
-        if (t1 > 0) {
-            const u32x4 k0 = kbuf[J][0], k1 = kbuf[J][1];
-            float s[G];  // scores, then p in place
-            bool trig = false;
-#pragma unroll
-            for (int h = 0; h < G; ++h) s[h] = sum8(dot16(k0, k1, qr[h][0], qr[h][1])) * a.scale_log2;
-            if (t1 < 8) {
-#pragma unroll
-                for (int h = 0; h < G; ++h) s[h] = t < t1 ? s[h] : -INFINITY;
-            }
-#pragma unroll
-            for (int h = 0; h < G; ++h) trig |= s[h] > m[h] + kTau;  // m = -inf: always
-            if (__builtin_amdgcn_ballot_w64(trig)) {
-#pragma unroll
-                for (int h = 0; h < G; ++h) {
-                    const float m_new = fmaxf(m[h], max_slots(s[h]));
-                    if (m_new > m[h]) {
-                        const float f = exp2_fast(m[h] - m_new);  // 0 from -inf
-#pragma unroll
-                        for (int e = 0; e < kAcc; ++e) acc[h][e] *= f;
-                        l[h] *= f;
-                        m[h] = m_new;
-                    }
-                }
-            }
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                s[h] = exp2_fast(s[h] - (m[h] == -INFINITY ? 0.f : m[h]));  // 0 for masked tokens
-                l[h] += s[h];
-            }
-            const u32x4 v0 = vbuf[J][0], v1 = vbuf[J][1];
+    float pp[G];     // p of window n - 1 (0 before a phase's first window)
+    VSlot vpend;     // V rows of window n - 1
+    int eypend = 0;  // packed table fields of window n - 1
+    auto pv_tok = [&](const float *p, const VSlot &vv) __attribute__((always_inline)) {
+        if constexpr (TOK) {
+            const u32x4 v0 = vv[0], v1 = vv[1];
             float vf[16];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -742,10 +697,84 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
 #pragma unroll
             for (int h = 0; h < G; ++h) {
 #pragma unroll
-                for (int e = 0; e < 16; ++e) acc[h][e] = fmaf(s[h], vf[e], acc[h][e]);
+                for (int e = 0; e < 16; ++e) acc[h][e] = fmaf(p[h], vf[e], acc[h][e]);
             }
         }
-        if (tab_last(ey)) close_seg(b);
+    };
+    auto step_tok = [&](auto jc, int n, int np) __attribute__((always_inline)) {
+      if constexpr (TOK) {
+        constexpr int J = decltype(jc)::value;
+        constexpr int JI = (J + D) % NB;  // window n + D, into the slot window n - 1 freed
+        const i32x2 ei = enext;
+        issue(ei, kbuf[JI][0], kbuf[JI][1], vbuf[JI]);
+        const int ey = eyr[J];
+        const int eyp = eypend;
+        eyr[JI] = __builtin_amdgcn_readfirstlane(ei[1]);
+        enext = n + D + 1 < np ? tab[n + D + 1] : i32x2{-1, 0};
+
+        const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
+        if (tab_first(ey)) {
+            // window n opens a segment: its q rows sit in the slot after the one of
+            // the segment window n - 1 may still close
+            const CK_LDS char *qrow = qs + (qslot + (tab_last(eyp) ? 1 : 0)) * G * (kD * 2) + c * 16;
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                qr[h][0] = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2));
+                qr[h][1] = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2) + 128);
+            }
+        }
+        float s[G];  // scores of window n, then its p
+        {
+            const u32x4 k0 = kbuf[J][0], k1 = kbuf[J][1];
+#pragma unroll
+            for (int h = 0; h < G; ++h) s[h] = sum8(dot16(k0, k1, qr[h][0], qr[h][1])) * a.scale_log2;
+        }
+        pv_tok(pp, vpend);
+        if (tab_last(eyp)) close_seg(tab_b(eyp));
+        vpend[0] = vbuf[J][0];
+        vpend[1] = vbuf[J][1];
+        eypend = ey;
+        if (tab_first(ey)) {
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                m[h] = -INFINITY;
+                l[h] = 0.f;
+#pragma unroll
+                for (int e = 0; e < kAcc; ++e) acc[h][e] = 0.f;
+            }
+        }
+        if (t1 < 8) {  // tokens past the sequence's end (all 8 when t1 = 0)
+#pragma unroll
+            for (int h = 0; h < G; ++h) s[h] = t < t1 ? s[h] : -INFINITY;
+        }
+        bool trig = false;
+#pragma unroll
+        for (int h = 0; h < G; ++h) trig |= s[h] > m[h] + kTau;  // m = -inf: always
+        if (__builtin_amdgcn_ballot_w64(trig)) {
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const float m_new = fmaxf(m[h], max_slots(s[h]));
+                if (m_new > m[h]) {
+                    const float f = exp2_fast(m[h] - m_new);  // 0 from -inf
+#pragma unroll
+                    for (int e = 0; e < kAcc; ++e) acc[h][e] *= f;
+                    l[h] *= f;
+                    m[h] = m_new;
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            pp[h] = exp2_fast(s[h] - (m[h] == -INFINITY ? 0.f : m[h]));  // 0 for masked tokens
+            l[h] += pp[h];
+        }
+      }
+    };
+    // after a phase's last window: its values and its segment's close
+    auto drain_tok = [&]() __attribute__((always_inline)) {
+      if constexpr (TOK) {
+        pv_tok(pp, vpend);
+        if (tab_last(eypend)) close_seg(tab_b(eypend));
       }
     };
 
@@ -787,7 +816,15 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             issue(e, kbuf[j][0], kbuf[j][1], vbuf[j]);
             if constexpr (TOK) eyr[j] = __builtin_amdgcn_readfirstlane(e[1]);
         }
-        if constexpr (TOK) enext = D < np ? tab[D] : i32x2{-1, 0};
+        if constexpr (TOK) {
+            enext = D < np ? tab[D] : i32x2{-1, 0};
+            // "window -1" of the pipelined step: no values, no close
+#pragma unroll
+            for (int h = 0; h < G; ++h) pp[h] = 0.f;
+            vpend[0] = u32x4{0u, 0u, 0u, 0u};
+            vpend[1] = u32x4{0u, 0u, 0u, 0u};
+            eypend = 0;
+        }
         // full rounds of NB steps, then the rest: the ring slot of every step is a
         // compile-time constant and no step leaves the loop early, so the
         // compiler's vmcnt bookkeeping sees one path around the back edge
@@ -806,6 +843,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                 else step(jc, n + decltype(jc)::value, np);
             }
         });
+        drain_tok();
         p0 = p1;
     }
 }
