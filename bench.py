@@ -44,7 +44,8 @@ MERGE_ROWS = 256 * 32        # [B=256, H=32] rows of D = 128
 NORM_M, NORM_K = 2048, 5120  # add_rms_norm_stats at the reference's prefill-main shape
 ROTATE_BYTES = 2 << 30
 # the kernels each op launches (an op's HIP-event time covers all of them)
-OP_KERNELS = {"fa_fp32_stage1": "stage1_kernel + stage1_combine_kernel",
+OP_KERNELS = {"cascade_decode": "cascade_fused_kernel + cascade_epilogue_kernel",
+              "fa_fp32_stage1": "stage1_kernel + stage1_combine_kernel",
               "suffix_decode": "suffix_stream_kernel + suffix_fixup_kernel",
               "lse_merge": "lse_merge_kernel"}
 CPU_THREADS_MAX = 16         # the GPU box's host-core share for one GPU
@@ -272,9 +273,15 @@ def main():
         "cascade_us": round(ms_step * 1e3, 2),
         "cascade_unfused_us": round(ms["cascade_unfused"] * 1e3, 2),
         "per_op_us": {k: round(v[0] * 1e3, 2) for k, v in per_op.items()},
-        "roofline": {"kernel": dom + " op (" + OP_KERNELS[dom] + ")", "bound": "hbm", "achieved": round(dom_gbs, 2),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic.get(dom)},
+        # the step's own launches: the fused kernel (stage-1 units and suffix streams
+        # side by side, most of the step's time) and its epilogue, timed together
+        "roofline": {"kernel": "cascade_decode op (" + OP_KERNELS["cascade_decode"] + ")", "bound": "hbm",
+                     "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic.get("cascade_decode")},
+        # the slowest op of the reference's three-op composition, for comparison
+        "roofline_ops": {"kernel": dom + " op (" + OP_KERNELS[dom] + ")", "bound": "hbm",
+                         "achieved": round(dom_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic.get(dom)},
     }
     if args.no_extras:
         print(json.dumps(line), flush=True)

@@ -864,56 +864,56 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_wide_kernel(SuffixArgs
 
 // Folds the partials of one query head of a sequence cut by chunk boundaries
 // (chunks ca < cb): the tail slot (1) of chunk ca and the head slot (0) of every
-// later chunk that holds windows, weighted by exp(lse - max). The first kPre
-// chunks' partials are loaded before any is used, so the usual 2-4 chunk case
-// costs one memory round trip; longer runs continue in a loop. The arithmetic
-// (max over all, then a weighted sum in chunk order) does not depend on kPre.
+// later chunk that holds windows, weighted by exp(lse - max). Online over batches
+// of kB chunks whose loads all go out before any is used: one memory round trip
+// per batch, not one per chunk (a long sequence spans many chunks, and the
+// slowest sequence sets the kernel's time).
 template <int G>
 __device__ __forceinline__ void fold_cut(const float *part_o, const float *part_lse, int g, const ChunkMap &cm,
                                          int hq, int d4, int ca, int cb, float4 &o_out, float &lse_out) {
-    constexpr int kPre = 4;
+    constexpr int kB = 8;
     auto pidx = [&](int ch, int sl) { return (((int64_t)g * cm.P + ch) * 2 + sl) * G + hq; };
-    // a chunk with no windows wrote nothing
-    auto empty_chunk = [&](int ch) { return cm.empty(ch); };
-    float pl[kPre];
-    float4 po[kPre];
-    bool ok[kPre];
-#pragma unroll
-    for (int j = 0; j < kPre; ++j) {
-        const int ch = min(ca + j, cb);  // clamped: every load is in bounds
-        ok[j] = ca + j <= cb && (j == 0 || !empty_chunk(ch));
-        const int64_t p = pidx(ch, j == 0 ? 1 : 0);
-        pl[j] = part_lse[p];
-        po[j] = *reinterpret_cast<const float4 *>(part_o + p * kD + 4 * d4);
-    }
-    float mx = pl[0];
-#pragma unroll
-    for (int j = 1; j < kPre; ++j)
-        if (ok[j]) mx = fmaxf(mx, pl[j]);
-    for (int ch = ca + kPre; ch <= cb; ++ch)
-        if (!empty_chunk(ch)) mx = fmaxf(mx, part_lse[pidx(ch, 0)]);
-    const float mu = mx == -INFINITY ? 0.f : mx;
+    float m = -INFINITY, wsum = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    float wsum = 0.f;
-    auto add = [&](float l, const float4 &o) {
-        const float wgt = exp2_fast((l - mu) * kLog2e);
-        acc.x = fmaf(wgt, o.x, acc.x);
-        acc.y = fmaf(wgt, o.y, acc.y);
-        acc.z = fmaf(wgt, o.z, acc.z);
-        acc.w = fmaf(wgt, o.w, acc.w);
-        wsum += wgt;
-    };
+    for (int c0 = ca; c0 <= cb; c0 += kB) {
+        float pl[kB];
+        float4 po[kB];
+        bool ok[kB];
 #pragma unroll
-    for (int j = 0; j < kPre; ++j)
-        if (ok[j]) add(pl[j], po[j]);
-    for (int ch = ca + kPre; ch <= cb; ++ch) {
-        if (empty_chunk(ch)) continue;
-        const int64_t p = pidx(ch, 0);
-        add(part_lse[p], *reinterpret_cast<const float4 *>(part_o + p * kD + 4 * d4));
+        for (int j = 0; j < kB; ++j) {
+            const int ch = min(c0 + j, cb);  // clamped: every load is in bounds
+            // a chunk with no windows wrote nothing (chunk ca holds the sequence's start)
+            ok[j] = c0 + j <= cb && (c0 + j == ca || !cm.empty(ch));
+            const int64_t p = pidx(ch, c0 + j == ca ? 1 : 0);
+            pl[j] = part_lse[p];
+            po[j] = *reinterpret_cast<const float4 *>(part_o + p * kD + 4 * d4);
+        }
+        float mb = m;
+#pragma unroll
+        for (int j = 0; j < kB; ++j)
+            if (ok[j]) mb = fmaxf(mb, pl[j]);
+        const float mu = mb == -INFINITY ? 0.f : mb;
+        const float r = exp2_fast((m - mu) * kLog2e);  // 0 from m = -inf
+        acc.x *= r;
+        acc.y *= r;
+        acc.z *= r;
+        acc.w *= r;
+        wsum *= r;
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+            if (!ok[j]) continue;
+            const float wgt = exp2_fast((pl[j] - mu) * kLog2e);
+            acc.x = fmaf(wgt, po[j].x, acc.x);
+            acc.y = fmaf(wgt, po[j].y, acc.y);
+            acc.z = fmaf(wgt, po[j].z, acc.z);
+            acc.w = fmaf(wgt, po[j].w, acc.w);
+            wsum += wgt;
+        }
+        m = mb;
     }
     const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
     o_out = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
-    lse_out = wsum > 0.f ? mx + __logf(wsum) : -INFINITY;
+    lse_out = wsum > 0.f ? m + __logf(wsum) : -INFINITY;
 }
 
 // One workgroup of 32 G threads per (sequence, kv head): empty suffixes get
