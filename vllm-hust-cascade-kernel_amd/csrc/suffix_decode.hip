@@ -114,6 +114,7 @@ constexpr int kFusedTokDepth = 2;  // token-major: 16 registers per window and l
 // Share of each fused workgroup's suffix windows that its streaming waves take
 // (in 1/256); the stage-1 waves take the rest after their stage-1 unit.
 constexpr int kFusedSplit = 192;
+static_assert(kFusedSplit >= 128 && kFusedSplit < 256, "ChunkMap::none_empty assumes a share in [1/2, 1)");
 
 // LDS layout (bytes) of the stream body for G query heads per group and NW waves
 template <int G, int NW>
@@ -198,6 +199,11 @@ struct ChunkMap {
         return 2 * j + (p >= lo(2 * j + 1) ? 1 : 0);
     }
     __device__ __forceinline__ bool empty(int c) const { return lo(c) == lo(c + 1); }
+    // No chunk is empty once there are at least as many windows as chunks: equal
+    // chunks then hold >= 1 window each, and each pair's range holds >= 2, of which
+    // a share split / 256 in [1/2, 1) leaves >= 1 to either chunk. (Saves the
+    // divisions of empty(), which dominated the fix-up's and epilogue's time.)
+    __device__ __forceinline__ bool none_empty() const { return W >= P; }
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -883,7 +889,7 @@ __device__ __forceinline__ void fold_cut(const float *part_o, const float *part_
         for (int j = 0; j < kB; ++j) {
             const int ch = min(c0 + j, cb);  // clamped: every load is in bounds
             // a chunk with no windows wrote nothing (chunk ca holds the sequence's start)
-            ok[j] = c0 + j <= cb && (c0 + j == ca || !cm.empty(ch));
+            ok[j] = c0 + j <= cb && (c0 + j == ca || cm.none_empty() || !cm.empty(ch));
             const int64_t p = pidx(ch, c0 + j == ca ? 1 : 0);
             pl[j] = part_lse[p];
             po[j] = *reinterpret_cast<const float4 *>(part_o + p * kD + 4 * d4);
