@@ -272,17 +272,6 @@ __device__ __forceinline__ int64_t clamp_len(const SuffixArgs &a, int64_t kvl) {
     return kvl < 0 ? 0 : kvl;
 }
 
-// Largest b in [0, batch] with cw[b] <= x (the sequence holding window x < W).
-__device__ __forceinline__ int seq_of_window(const CK_LDS int *cw, int batch, int x) {
-    int lo = 0, hi = batch;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (cw[mid] <= x) lo = mid;
-        else hi = mid - 1;
-    }
-    return lo;
-}
-
 // The stream body on NW waves (thread tid of the group's NW * 64) as workgroup lb
 // of a grid of a.kv_heads * a.chunks, with the group's LDS at smem and its own
 // barrier. Windows hold 8 NW tokens.
@@ -397,10 +386,15 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         }
     };
     // the next non-empty sequence after b that starts inside [w0, w1), or -1
-    auto next_seg = [&](int b) {
-        ++b;
-        while (b < a.batch && cw[b + 1] == cw[b]) ++b;
-        return (b < a.batch && cw[b] < w1) ? b : -1;
+    // Largest b in [0, batch] with cw[b] <= x: two ballots over the wave's lanes
+    // (a stride-S sample of cw, then the S entries after the last sample <= x)
+    // instead of a binary search of ~10 dependent LDS reads.
+    auto find_seq = [&](int x) {
+        const int S = (a.batch + 64) / 64;  // 64 S > batch
+        const uint64_t m1 = __builtin_amdgcn_ballot_w64(cw[min(lane * S, a.batch)] <= x);
+        const int base = (__builtin_popcountll(m1) - 1) * S;  // cw is nondecreasing, cw[0] = 0 <= x
+        const uint64_t m2 = __builtin_amdgcn_ballot_w64(lane < S && cw[min(base + lane, a.batch)] <= x);
+        return base + __builtin_popcountll(m2) - 1;
     };
 
     // ---- per-lane constants ------------------------------------------------------------
@@ -792,23 +786,51 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             wait_vmcnt<0>();
             bar.sync();  // every wave is done with the previous phase's table and q rows
         }
-        int bq = seq_of_window(cw, a.batch, w0 + p0);  // the phase's first segment
-        int nseg = 0;
-        while (bq >= 0 && nseg < kQSlots) {
-            if (nseg % NW == wid) dma_q(bq, nseg);
-            ++nseg;
-            bq = next_seg(bq);
+        // The phase's segments: the first kQSlots non-empty sequences from the one
+        // holding window w0 + p0 that start inside the chunk, read from one ballot
+        // over 64 candidate sequences (every wave finds the same list on its own).
+        const int bq0 = find_seq(w0 + p0);  // non-empty: cw[bq0 + 1] > w0 + p0
+        const int bc = min(bq0 + lane, a.batch - 1);
+        const int c_lo = cw[bc], c_hi = cw[bc + 1], c_len = len[bc];
+        uint64_t segm = __builtin_amdgcn_ballot_w64(bq0 + lane < a.batch && c_hi > c_lo && c_lo < w1);
+        int segb[kQSlots], seg_lo[kQSlots], seg_hi[kQSlots], seg_len[kQSlots];
+#pragma unroll
+        for (int sg = 0; sg < kQSlots; ++sg) {
+            seg_lo[sg] = 0x7FFFFFFF;  // never selected below
+            segb[sg] = seg_hi[sg] = seg_len[sg] = 0;
+            if (segm != 0) {
+                const int l = __builtin_ctzll(segm);
+                segm &= segm - 1;
+                segb[sg] = bq0 + l;
+                seg_lo[sg] = __builtin_amdgcn_readlane(c_lo, l);
+                seg_hi[sg] = __builtin_amdgcn_readlane(c_hi, l);
+                seg_len[sg] = __builtin_amdgcn_readlane(c_len, l);
+                if (sg % NW == wid) dma_q(segb[sg], sg);
+            }
         }
         int p1 = min(p0 + kTable, nwin);
-        if (bq >= 0) p1 = min(p1, cw[bq] - w0);  // the next segment opens the next phase
+        if (segm != 0) {
+            p1 = min(p1, __builtin_amdgcn_readlane(c_lo, __builtin_ctzll(segm)) - w0);  // the next segment opens the next phase
+        } else if (bq0 + 64 < a.batch) {
+            p1 = min(p1, cw[bq0 + 64] - w0);  // candidates beyond the 64 examined: the next phase
+        }
         const int np = p1 - p0;
         for (int i = tid; i < np; i += kThr) {
             const int wg = w0 + p0 + i;
-            const int b = seq_of_window(cw, a.batch, wg);
-            const int k = wg - cw[b];
-            const int tv = min(len[b] - k * kWin, kWin);
-            const int first = wg == max(cw[b], w0);
-            const int last = wg == min(cw[b + 1], w1) - 1;
+            int b = segb[0], lo_b = seg_lo[0], hi_b = seg_hi[0], len_b = seg_len[0];
+#pragma unroll
+            for (int sg = 1; sg < kQSlots; ++sg) {
+                if (seg_lo[sg] <= wg) {  // the last segment starting at or before window wg
+                    b = segb[sg];
+                    lo_b = seg_lo[sg];
+                    hi_b = seg_hi[sg];
+                    len_b = seg_len[sg];
+                }
+            }
+            const int k = wg - lo_b;
+            const int tv = min(len_b - k * kWin, kWin);
+            const int first = wg == max(lo_b, w0);
+            const int last = wg == min(hi_b, w1) - 1;
             const int page = a.bt[(int64_t)b * a.bt_cols + k / kWpp];
             const bool ok = page >= 0 && (int64_t)page < a.num_blocks;
             tab[i] = i32x2{ok ? page : -1, tv | (first << 7) | (last << 8) | ((k % kWpp) << 9) | (b << 11)};
