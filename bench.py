@@ -148,7 +148,7 @@ def cpu_baseline(torch):
     step()  # warm-up
     times = []
     t_start = time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - t_start < 10.0 and len(times) < 200):
+    while len(times) < 5 or (time.perf_counter() - t_start < 12.0 and len(times) < 2000):
         t0 = time.perf_counter()
         step()
         times.append(time.perf_counter() - t0)

@@ -385,7 +385,6 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                       qs + slot * G * (kD * 2) + u0 * 16);
         }
     };
-    // the next non-empty sequence after b that starts inside [w0, w1), or -1
     // Largest b in [0, batch] with cw[b] <= x: two ballots over the wave's lanes
     // (a stride-S sample of cw, then the S entries after the last sample <= x)
     // instead of a binary search of ~10 dependent LDS reads.
