@@ -20,20 +20,25 @@
 //   computed in registers in fp32 and stored once as bf16 -- the gate/up
 //   product never reaches memory.
 // * Main kernel (K a multiple of 32): workgroup tile 256 activation rows x
-//   (128 gate + the matching 128 up weight rows), K step 32, 4 waves (one per
-//   SIMD) arranged 2 (activation) x 2 (weight); each wave owns 128 activation
-//   rows x (64 gate + 64 up) weight rows, 16 accumulator tiles of 32x32 in the
+//   (128 gate + the matching 128 up weight rows), 4 waves (one per SIMD)
+//   arranged 2 (activation) x 2 (weight); each wave owns 128 activation rows x
+//   (64 gate + 64 up) weight rows, 16 accumulator tiles of 32x32 in the
 //   accumulation registers, so per 16-deep k-substep 8 fragment reads feed 16
 //   MFMAs (half an LDS read per MFMA). Operand tiles stream global -> LDS by
 //   DMA (global_load_lds_dwordx4: no staging registers, no LDS write
-//   instructions) into a 4 x 32 KB ring, three tiles ahead; each 64-byte row
-//   is XOR-swizzled at 16-byte granularity (the DMA lane fetches the chunk that
+//   instructions). With K a multiple of 64 a stage is 64 deep, so each staged
+//   row is one whole 128-byte line and a DMA instruction fetches 8 whole lines
+//   (with 32-deep stages it fetched 16 half lines: the address unit's cost per
+//   byte doubles, and it bounded the kernel). Two such 64-KB stages would fill
+//   the ring, so the ring is five 32-KB parts, one operand of one stage each:
+//   the weights run two tiles ahead, the activations one. Rows are
+//   XOR-swizzled at 16-byte granularity (the DMA lane fetches the chunk that
 //   belongs at its LDS slot) so the 32-row fragment reads are bank-conflict
-//   free. The fragments of substep s + 1 are read while the
-//   MFMAs of substep s run, interleaved by scheduling barriers. A half-width
-//   instance (64 gate + 64 up rows, 24 KB stages) runs when the full-width grid
-//   would leave CUs idle (a few m-tiles, e.g. M = 256 at I = 14336: 224
-//   workgroups instead of 112).
+//   free. The fragments of substep s + 1 are read while the MFMAs of substep s
+//   run, interleaved by scheduling barriers. A half-width instance (64 gate +
+//   64 up rows, three 48-KB stages) runs when the full-width grid would leave
+//   CUs idle (a few m-tiles, e.g. M = 256 at I = 14336: 224 workgroups instead
+//   of 112). K = 32 mod 64 runs the same kernel on 32-deep stages (4-stage ring).
 // * Decode-sized kernel (M <= 32, K % 256 == 0): the weight stream bounds the
 //   op, so a workgroup takes 32 gate + 32 up rows (I / 32 workgroups, two per
 //   CU) and its 4 waves each stream a quarter of K from global memory straight
@@ -203,43 +208,62 @@ __global__ __launch_bounds__(kThreads) void gateup_general_kernel(GemmArgs p) {
     }
 }
 
-// ---- main kernel: 4 waves x (128 x 64 WB), DMA-fed 4-stage LDS ring ---------------------
+// ---- main kernel: 4 waves x (128 x 64 WB), DMA-fed LDS ring ---------------------------
 constexpr int kDThreads = 256;
-constexpr int kDBK = 32;                                  // K per ring stage
-constexpr int kDStages = 4;
 constexpr int kGroupM = 4;   // tile block one XCD runs at once: 4 m-tiles x 8 n-tiles
 constexpr int kGroupN = 8;
-constexpr int kDRowBytes = kDBK * 2;                      // 64 B per staged row
 
 // Workgroup tile of the DMA kernel: 256 activation rows x WB * 64 gate rows (and as
 // many up rows); each wave holds WB 32-row blocks of gate and of up. WB = 2 is the
 // 256 x (128 + 128) tile; WB = 1 halves the weight rows so that a small M (one
-// m-tile) still spreads over twice the workgroups.
-template <int WB>
+// m-tile) still spreads over twice the workgroups. BK = K per ring stage: 64 (rows
+// of 128 bytes, one whole cache line per row and DMA lane group) when K allows,
+// else 32 (64-byte rows). The ring holds as many stages as fit in 160 KB, at most 4.
+template <int WB, int BK>
 struct DmaTile {
-    static constexpr int kNh = 64 * WB;                              // gate rows per workgroup
-    static constexpr int kStageBytes = (kBM + 2 * kNh) * kDRowBytes;  // 32 KB (WB 2) / 24 KB (WB 1)
-    static constexpr int kDmaPerWave = kStageBytes / 1024 / 4;        // 8 / 6
-    static constexpr int kLdsBytes = kDStages * kStageBytes;          // 128 KB / 96 KB
-    static constexpr int kMfmaHalf = 8 * WB;                          // MFMAs per wave per K half
-    static constexpr int kReads = 2 * WB + 4;                         // fragment reads per K half
+    static constexpr int kNh = 64 * WB;                               // gate rows per workgroup
+    static constexpr int kRowBytes = BK * 2;                          // 128 / 64 B per staged row
+    static constexpr int kRows = kBM + 2 * kNh;                       // staged rows per stage
+    static constexpr int kStageBytes = kRows * kRowBytes;             // 64 / 48 KB (BK 64), 32 / 24 KB (BK 32)
+    static constexpr int kStages = BK == 64 ? (WB == 2 ? 2 : 3) : 4;
+    static constexpr int kDmaPerWave = kStageBytes / 1024 / 4;        // 16 / 12 (BK 64), 8 / 6 (BK 32)
+    static constexpr int kRowsPerDma = 1024 / kRowBytes;              // 8 / 16 rows per 1-KB DMA
+    // 256 x (128 + 128) at BK 64: two 64-KB stages would be all the ring holds, so
+    // the operands get rings of their own within five 32-KB parts instead (below)
+    static constexpr bool kSplit = BK == 64 && WB == 2;
+    static constexpr int kPart = kBM * kRowBytes;                     // 32 KB: one operand of one stage
+    static constexpr int kLdsBytes = kSplit ? 5 * kPart : kStages * kStageBytes;  // 160 / 144 KB, 128 / 96 KB
+    static constexpr int kSub = BK / 16;                              // 16-deep MFMA substeps per stage
+    static constexpr int kMfmaSub = 8 * WB;                           // MFMAs per wave per substep
+    static constexpr int kReads = 2 * WB + 4;                         // fragment reads per substep
+    // DMAs of a stage issued right after the barrier that frees its slot (in the
+    // stage's last substep); the rest go out in the first substep of the next stage
+    static constexpr int kEarlyDma = BK == 64 && WB == 2 ? kDmaPerWave : kDmaPerWave / 2;
+    static_assert(kLdsBytes <= 160 * 1024, "ring fits the LDS");
 };
 
-// Byte offset of 16-byte chunk ch of staged row `row`: 64-byte rows, chunk
-// slot ch ^ f(row) with f(row) = ((row >> 1) ^ (row >> 2)) & 3. A fragment read
-// has 32 lanes on consecutive rows at one chunk; with this f the rows that
-// share a bank window -- 4 per 256-byte window (16 lanes per LDS cycle) or 2
-// per 128-byte window -- land on different 16-byte slots, so the read is
-// conflict-free (a plain ((row >> 1) & 3) collides rows r and r + 8).
-__device__ __forceinline__ int dsw_swz(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
-__device__ __forceinline__ int dsw_off(int row, int ch) { return row * kDRowBytes + ((ch ^ dsw_swz(row)) << 4); }
+// Byte offset of 16-byte chunk ch of staged row `row`: chunk slot ch ^ f(row). A
+// fragment read has 32 lanes on consecutive rows at one chunk, 16 lanes per LDS
+// cycle over 256-byte bank windows: with 128-byte rows (two per window) f(row) =
+// (row >> 1) & 7 puts the 16 rows of a cycle on 16 distinct 16-byte slots; with
+// 64-byte rows (four per window) f(row) = ((row >> 1) ^ (row >> 2)) & 3 does (a
+// plain ((row >> 1) & 3) collides rows r and r + 8).
+template <int BK>
+__device__ __forceinline__ int dsw_swz(int row) {
+    if constexpr (BK == 64) return (row >> 1) & 7;
+    else return ((row >> 1) ^ (row >> 2)) & 3;
+}
+template <int BK>
+__device__ __forceinline__ int dsw_off(int row, int ch) { return row * (BK * 2) + ((ch ^ dsw_swz<BK>(row)) << 4); }
 
-template <int MODE, int WB>
+template <int MODE, int WB, int BK>
 __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
-    using T = DmaTile<WB>;
+    using T = DmaTile<WB, BK>;
     constexpr int kBNhW = T::kNh;
-    constexpr int kDStageBytes = T::kStageBytes;
-    constexpr int kDDmaPerWave = T::kDmaPerWave;
+    constexpr int kS = T::kStages;
+    constexpr int kNS = T::kSub;
+    constexpr int kD = T::kDmaPerWave;
+    constexpr int kRB = T::kRowBytes;
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
     CK_LDS char *smem = (CK_LDS char *)smem_raw;
     const int tid = threadIdx.x;
@@ -266,18 +290,22 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
     }
     const int64_t m0 = (int64_t)mi * kBM;
     const int64_t n0 = (int64_t)ni * kBNhW;
-    const int ktiles = (int)(p.k / kDBK);
+    const int ktiles = (int)(p.k / BK);
 
-    // DMA geometry: instruction j of wave w fills staged rows 16*(8w + j) .. +16
-    // (waves 0-1: activations, wave 2: gate rows, wave 3: up rows); lane l ->
-    // row + l/4, LDS slot l%4, which holds global chunk (l%4) ^ f(row); rows of
-    // an instruction start at a multiple of 16, so f(row) = f(l/4).
-    const int rsub = lane >> 2;
-    const int coff = ((lane & 3) ^ dsw_swz(rsub)) * 8;
-    const uint16_t *gp[kDDmaPerWave];
+    // DMA geometry: instruction j of wave w fills the kRowsPerDma staged rows from
+    // R0 = kRowsPerDma (kD w + j) (waves 0-1: activations, wave 2: gate rows, wave 3:
+    // up rows); lane l -> row R0 + l / (kRB / 16), LDS slot l % (kRB / 16), which holds
+    // global chunk slot ^ f(row): every lane group reads one whole row segment.
+    constexpr int kLpr = kRB / 16;  // lanes per staged row
+    // Split ring (T::kSplit): DMA j < kD / 2 of wave w fills activation rows from
+    // 8 (kD / 2 w + j), the others weight rows from 8 (kD / 2 w + j - kD / 2), in
+    // the parts of their own operand.
+    const uint16_t *gp[kD];
 #pragma unroll
-    for (int j = 0; j < kDDmaPerWave; ++j) {
-        const int R = 16 * (kDDmaPerWave * wid + j) + rsub;
+    for (int j = 0; j < kD; ++j) {
+        const int R = T::kSplit ? (j < kD / 2 ? 0 : kBM) + 8 * ((kD / 2) * wid + j % (kD / 2)) + lane / kLpr
+                                : T::kRowsPerDma * (kD * wid + j) + lane / kLpr;
+        const int coff = ((lane % kLpr) ^ dsw_swz<BK>(R)) * 8;
         int64_t grow;
         const uint16_t *base;
         if (R < kBM) {
@@ -303,89 +331,125 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
 
     // DMA j of this wave: K tile `src` into the ring slot of tile `slot`
     auto dma_one = [&](int slot, int src, int j) {
-        CK_LDS char *dst = smem + (slot % kDStages) * kDStageBytes + (kDDmaPerWave * wid) * 1024;
-        dma16(gp[j] + (int64_t)src * kDBK, dst + j * 1024);
+        CK_LDS char *dst = smem + (slot % kS) * T::kStageBytes + (kD * wid) * 1024;
+        dma16(gp[j] + (int64_t)src * BK, dst + j * 1024);
     };
-    static_assert(kDBK == 32 && kDDmaPerWave % 2 == 0 && kDDmaPerWave / 2 <= T::kMfmaHalf / 2,
-                  "two K halves per tile, half the DMAs in each, at most one per MFMA pair");
-    // fragment read r of K half s of the tile in ring slot `slot`: r < 2 WB -> weight
+    // Split ring: part q holds the weights of tile q / 2 (q even) or its
+    // activations (q odd) in slot q % 5, so the weight rows of tile t sit in
+    // slot 2t % 5 and its activation rows in (2t + 1) % 5.
+    auto wslot = [&](int t) { return smem + ((2 * t) % 5) * T::kPart; };
+    auto aslot = [&](int t) { return smem + ((2 * t + 1) % 5) * T::kPart; };
+    auto dma_w = [&](int t, int src, int jj) {  // weight DMA jj of tile t
+        dma16(gp[kD / 2 + jj] + (int64_t)src * BK, wslot(t) + ((kD / 2) * wid + jj) * 1024);
+    };
+    auto dma_a = [&](int t, int src, int jj) {  // activation DMA jj of tile t
+        dma16(gp[jj] + (int64_t)src * BK, aslot(t) + ((kD / 2) * wid + jj) * 1024);
+    };
+    constexpr int kLate = kD - T::kEarlyDma;
+    constexpr int kSpE = T::kMfmaSub / T::kEarlyDma > 1 ? T::kMfmaSub / T::kEarlyDma : 1;  // MFMAs per early DMA
+    constexpr int kSpL = kLate > 0 && T::kMfmaSub / kLate > 1 ? T::kMfmaSub / kLate : 1;     // MFMAs per late DMA
+    static_assert(kLate <= T::kMfmaSub && T::kEarlyDma <= T::kMfmaSub && T::kEarlyDma > 0,
+                  "at most one DMA per MFMA");
+    // fragment read r of substep s of the tile in ring slot `slot`: r < 2 WB -> weight
     // block (gb, gu) = (r >> 1, r & 1), r >= 2 WB -> activation block r - 2 WB
 #define CK_GEMM_READ(slot, s, r, WF, XF)                                                                      \
     do {                                                                                                      \
-        const CK_LDS char *xa_ = smem + ((slot) % kDStages) * kDStageBytes;                                   \
+        const CK_LDS char *xa_ = T::kSplit ? aslot(slot) : smem + ((slot) % kS) * T::kStageBytes;             \
+        const CK_LDS char *xw_ = T::kSplit ? wslot(slot) : xa_ + kBM * kRB;                                   \
         const int ch_ = 2 * (s) + hh;                                                                         \
         if ((r) < 2 * WB)                                                                                     \
             WF[(r) >> 1][(r) & 1] = *reinterpret_cast<const CK_LDS bf16x8 *>(                                  \
-                xa_ + kBM * kDRowBytes + dsw_off(((r) & 1) * kBNhW + ww * 32 * WB + ((r) >> 1) * 32 + l32, ch_)); \
+                xw_ + dsw_off<BK>(((r) & 1) * kBNhW + ww * 32 * WB + ((r) >> 1) * 32 + l32, ch_));             \
         else                                                                                                  \
             XF[(r) - 2 * WB] = *reinterpret_cast<const CK_LDS bf16x8 *>(                                      \
-                xa_ + dsw_off(wa * 128 + ((r) - 2 * WB) * 32 + l32, ch_));                                    \
+                xa_ + dsw_off<BK>(wa * 128 + ((r) - 2 * WB) * 32 + l32, ch_));                                \
     } while (0)
-    // Reads in the order the next half's MFMAs consume them: MFMA 0 needs weight
+    // Reads in the order the next substep's MFMAs consume them: MFMA 0 needs weight
     // block 0 and activation block 0, then the other weight blocks one per MFMA,
     // then one activation block every 2 WB MFMAs, so every wait is partial.
     constexpr int kReadOrder[8] = {0, 2 * WB, 1, WB == 2 ? 2 : 3, WB == 2 ? 3 : 4, WB == 2 ? 5 : 5, 6, 7};
-    // MFMA i of a K half: (ab, gb, gu) = (i / 2WB, (i / 2) % WB, i % 2)
+    // MFMA i of a substep: (ab, gb, gu) = (i / 2WB, (i / 2) % WB, i % 2)
 #define CK_GEMM_MFMA(i, WF, XF)                                                                               \
     acc[(i) / (2 * WB)][((i) >> 1) % WB][(i) & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(                  \
         WF[((i) >> 1) % WB][(i) & 1], XF[(i) / (2 * WB)], acc[(i) / (2 * WB)][((i) >> 1) % WB][(i) & 1], 0, 0, 0)
 
-    // DMA schedule: the 8 DMAs of tile t go out in two halves of 4, the first
-    // after the barrier of iteration t - 4 (which frees tile t - 4's slot), the
-    // second in the first K half of iteration t - 3, so the address unit sees
-    // 4 DMAs per wave in every K half instead of 8 in one. A tile index past the
-    // end repeats the last tile into a slot nothing reads again.
-    constexpr int kHalfDma = kDDmaPerWave / 2;
-    // prologue: tiles 0-2 and the first half of tile 3 in flight, tile 0 landed
-    for (int t = 0; t < kDStages; ++t)
+    // DMA schedule: tile t + kS goes into tile t's slot, freed by the barrier in
+    // tile t's last substep; kEarlyDma of its DMAs go out right after that barrier,
+    // the rest in the first substep of tile t + 1. A tile index past the end repeats
+    // the last tile into a slot nothing reads again, so every tile issues the same
+    // DMAs and the vmcnt waits are exact.
+    //   Split ring: weights run two tiles ahead, activations one. The weights of
+    // tile t + 2 go out in tile t's first substep, into the part tile t - 1's
+    // activations left at the barrier of tile t - 1; the activations of tile t + 2
+    // in its last substep, into the part of tile t's weights, freed by the barrier
+    // just before. At the barrier of tile t only the weights of tile t + 2 may
+    // still be in flight.
+    // prologue: tiles 0 .. kS-2 and the early DMAs of tile kS - 1 in flight (split:
+    // tiles 0 and 1), tile 0 landed
+    if constexpr (T::kSplit) {
 #pragma unroll
-        for (int j = 0; j < kDDmaPerWave; ++j)
-            if (t < kDStages - 1 || j < kHalfDma) dma_one(t, min(t, ktiles - 1), j);
-    wait_vmcnt<(kDStages - 2) * kDDmaPerWave + kHalfDma>();
-    __syncthreads();
-    bf16x8 wf0[WB][2], xf0[4], wf1[WB][2], xf1[4];
+        for (int t = 0; t < 2; ++t) {
+            const int src = min(t, ktiles - 1);
 #pragma unroll
-    for (int r = 0; r < T::kReads; ++r) CK_GEMM_READ(0, 0, kReadOrder[r], wf0, xf0);
-    // Each tile: 32 MFMAs in two K halves with the other work placed between
-    // them in a fixed order (sched_barrier fences), so the wave issues its
-    // reads, address arithmetic and DMAs while the matrix pipe is busy:
-    //   half 0: MFMA on (kt, 0) + a read of (kt, 1) after every second MFMA and
-    //           DMAs 4-7 of tile kt + 3 (into tile kt - 1's slot) between;
-    //   barrier: every read of tile kt is done, tile kt + 1 has landed;
-    //   half 1: MFMA on (kt, 1) + a read of (kt + 1, 0) after every second MFMA
-    //           and DMAs 0-3 of tile kt + 4 (into tile kt's slot) between.
-    for (int kt = 0; kt < ktiles; ++kt) {
-        const int ta = min(kt + kDStages - 1, ktiles - 1);
+            for (int jj = 0; jj < kD / 2; ++jj) dma_w(t, src, jj);
 #pragma unroll
-        for (int i = 0; i < T::kMfmaHalf; ++i) {
-            CK_GEMM_MFMA(i, wf0, xf0);
-            if (WB == 2) {
-                if (i % 2 == 0) CK_GEMM_READ(kt, 1, kReadOrder[i / 2], wf1, xf1);
-                else if (i % 4 == 1) dma_one(kt + kDStages - 1, ta, kHalfDma + i / 4);
-            } else {
-                if (i < T::kReads) CK_GEMM_READ(kt, 1, kReadOrder[i], wf1, xf1);
-                if (i % 2 == 1 && i / 2 < kHalfDma) dma_one(kt + kDStages - 1, ta, kHalfDma + i / 2);
-            }
-            __builtin_amdgcn_sched_barrier(0);
+            for (int jj = 0; jj < kD / 2; ++jj) dma_a(t, src, jj);
         }
-        // tile kt + 1 has landed once at most the DMAs of tiles kt + 2 and kt + 3
-        // (issued earlier, real or repeated) remain in flight. In the last
-        // iteration the reads below fetch an unused slot and the DMAs repeat the
-        // last tile into tile kt's slot, which nothing reads again.
-        wait_vmcnt<(kDStages - 2) * kDDmaPerWave>();
-        __syncthreads();
-        const int tb = min(kt + kDStages, ktiles - 1);
+        wait_vmcnt<kD>();
+    } else {
+        for (int t = 0; t < kS; ++t)
 #pragma unroll
-        for (int i = 0; i < T::kMfmaHalf; ++i) {
-            CK_GEMM_MFMA(i, wf1, xf1);
-            if (WB == 2) {
-                if (i % 2 == 0) CK_GEMM_READ(kt + 1, 0, kReadOrder[i / 2], wf0, xf0);
-                else if (i % 4 == 1) dma_one(kt + kDStages, tb, i / 4);  // tile kt's slot: its reads are done
-            } else {
-                if (i < T::kReads) CK_GEMM_READ(kt + 1, 0, kReadOrder[i], wf0, xf0);
-                if (i % 2 == 1 && i / 2 < kHalfDma) dma_one(kt + kDStages, tb, i / 2);
+            for (int j = 0; j < kD; ++j)
+                if (t < kS - 1 || j < T::kEarlyDma) dma_one(t, min(t, ktiles - 1), j);
+        wait_vmcnt<(kS - 2) * kD + T::kEarlyDma>();
+    }
+    __syncthreads();
+    bf16x8 wf[2][WB][2], xf[2][4];
+#pragma unroll
+    for (int r = 0; r < T::kReads; ++r) CK_GEMM_READ(0, 0, kReadOrder[r], wf[0], xf[0]);
+    // Substep s of tile kt: its MFMAs with the next substep's fragment reads (tile
+    // kt + 1's first substep after the last) and the DMAs between them, in a fixed
+    // order (sched_barrier fences), so the wave issues its reads, address arithmetic
+    // and DMAs while the matrix pipe is busy. Before the last substep: tile kt + 1
+    // has landed and every read of tile kt is done (vmcnt wait + barrier).
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int ta = min(kt + kS - 1, ktiles - 1);  // late DMAs: tile kt + kS - 1
+        const int tb = min(kt + kS, ktiles - 1);      // early DMAs: tile kt + kS
+        const int t2 = min(kt + 2, ktiles - 1);       // split ring: tile kt + 2
+#pragma unroll
+        for (int s = 0; s < kNS; ++s) {
+            if (s == kNS - 1) {
+                // tile kt + 1 has landed once only the DMAs of tiles kt + 2 .. kt + kS - 1
+                // (real or repeated; split: the weights of tile kt + 2) remain in flight
+                if constexpr (T::kSplit) wait_vmcnt<kD / 2>();
+                else wait_vmcnt<(kS - 2) * kD>();
+                __syncthreads();
             }
-            __builtin_amdgcn_sched_barrier(0);
+            const int cur = s & 1, nxt = cur ^ 1;
+            const int rslot = s == kNS - 1 ? kt + 1 : kt;
+            const int rs = s == kNS - 1 ? 0 : s + 1;
+#pragma unroll
+            for (int i = 0; i < T::kMfmaSub; ++i) {
+                CK_GEMM_MFMA(i, wf[cur], xf[cur]);
+                if (WB == 2) {
+                    if (i % 2 == 0) CK_GEMM_READ(rslot, rs, kReadOrder[i / 2], wf[nxt], xf[nxt]);
+                } else {
+                    if (i < T::kReads) CK_GEMM_READ(rslot, rs, kReadOrder[i], wf[nxt], xf[nxt]);
+                }
+                if constexpr (T::kSplit) {
+                    // every second MFMA: weights of tile kt + 2 in substep 0,
+                    // activations of tile kt + 2 in the last substep
+                    if (s == 0 && i % 2 == 1) dma_w(kt + 2, t2, i / 2);
+                    if (s == kNS - 1 && i % 2 == 1) dma_a(kt + 2, t2, i / 2);
+                } else {
+                    // late DMAs spread over substep 0, early ones over the last substep
+                    if (s == 0 && i % kSpL == (kSpL > 1 ? 1 : 0) && i / kSpL < kLate)
+                        dma_one(kt + kS - 1, ta, T::kEarlyDma + i / kSpL);
+                    if (s == kNS - 1 && i % kSpE == (kSpE > 1 ? 1 : 0) && i / kSpE < T::kEarlyDma)
+                        dma_one(kt + kS, tb, i / kSpE);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
 #undef CK_GEMM_READ
@@ -583,15 +647,17 @@ __global__ __launch_bounds__(256) void gate_window_copy_kernel(const uint16_t *c
 
 constexpr int64_t kNumCus = 256;  // MI355X
 
-template <int MODE, int WB>
+template <int MODE, int WB, int BK>
 int launch_dma(GemmArgs p, hipStream_t s) {
-    using T = DmaTile<WB>;
+    using T = DmaTile<WB, BK>;
     p.ntiles = (int)(p.n_half / T::kNh);
     const int64_t grid = (int64_t)p.mtiles * p.ntiles;
     static std::atomic<uint64_t> lds_set{0};
-    int rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&gateup_dma_kernel<MODE, WB>), T::kLdsBytes, lds_set);
+    int rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&gateup_dma_kernel<MODE, WB, BK>), T::kLdsBytes,
+                                lds_set);
     if (rc != CK_OK) return rc;
-    hipLaunchKernelGGL((gateup_dma_kernel<MODE, WB>), dim3((unsigned)grid), dim3(kDThreads), T::kLdsBytes, s, p);
+    hipLaunchKernelGGL((gateup_dma_kernel<MODE, WB, BK>), dim3((unsigned)grid), dim3(kDThreads), T::kLdsBytes, s,
+                       p);
     CK_RETURN_LAUNCH();
 }
 
@@ -607,15 +673,17 @@ int launch_gemm(const GemmArgs &p, hipStream_t s) {
         CK_RETURN_LAUNCH();
     }
     const int64_t grid = (int64_t)p.mtiles * p.ntiles;
-    if (p.k % kDBK == 0) {
+    if (p.k % 32 == 0) {
         // The half-width tile (WB = 1) does about 3/4 of the full tile's work per
         // workgroup (its DMA bytes; half the MFMAs) with twice the workgroups: it
         // wins when it needs fewer than 4/3 as many rounds of resident workgroups
         // (one per CU), i.e. when the full-width grid leaves CUs idle.
         const int64_t rounds2 = (grid + kNumCus - 1) / kNumCus;
         const int64_t rounds1 = (2 * grid + kNumCus - 1) / kNumCus;
-        if (3 * rounds1 < 4 * rounds2) return launch_dma<MODE, 1>(p, s);
-        return launch_dma<MODE, 2>(p, s);
+        const bool half = 3 * rounds1 < 4 * rounds2;
+        // 128-byte staged rows (whole cache lines per DMA lane group) when K allows
+        if (p.k % 64 == 0) return half ? launch_dma<MODE, 1, 64>(p, s) : launch_dma<MODE, 2, 64>(p, s);
+        return half ? launch_dma<MODE, 1, 32>(p, s) : launch_dma<MODE, 2, 32>(p, s);
     }
     static std::atomic<uint64_t> lds_set_g{0};
     int rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&gateup_general_kernel<MODE>), 2 * kTileBytes,
