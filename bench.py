@@ -329,7 +329,7 @@ def main():
 
     def gemm(i):
         torch.ops.npu.f3_gateup_epilogue(a, wt, None, d_out, 1)
-    for _ in range(10):  # let the clocks settle under a sustained MFMA load before timing
+    for _ in range(40):  # let the clocks settle under a sustained MFMA load (~30 ms) before timing
         gemm(0)
     t_gemm = timed(gemm, max(20, n // 5))
     gemm_tflops = 2.0 * GEMM_M * GEMM_K * 2 * GEMM_I / (t_gemm * 1e-3) / 1e12
