@@ -267,7 +267,7 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
     CK_LDS char *smem = (CK_LDS char *)smem_raw;
     const int tid = threadIdx.x;
-    const int wid = tid >> 6;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: LDS addresses in SGPRs
     const int lane = tid & 63;
     const int hh = lane >> 5;
     const int l32 = lane & 31;
