@@ -56,6 +56,32 @@ __device__ __forceinline__ void dma16(const void *g, CK_LDS void *lds_base) {
                  : "memory", "m0");
 }
 
+// A raw buffer resource (V#) for `bytes` bytes from `base`: the 4 dwords
+// buffer_load takes in SGPRs (wave-uniform by construction). Reads past
+// `bytes` return zeros.
+typedef int ck_rsrc_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ ck_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    ck_rsrc_t r;
+    r[0] = (int)__builtin_amdgcn_readfirstlane((uint32_t)a);
+    r[1] = (int)(__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) & 0xffffu);  // stride 0
+    r[2] = (int)__builtin_amdgcn_readfirstlane(bytes);
+    r[3] = 0x00020000;
+    return r;
+}
+
+// 16-byte buffer -> LDS DMA (buffer_load_dwordx4 ... lds): lane l reads
+// rsrc.base + voff(l) + soff and its 16 bytes land at lds_base + 16 * l; voff is
+// a per-lane 32-bit offset, soff and lds_base wave-uniform. Inline asm like dma16.
+__device__ __forceinline__ void dma16_buf(const ck_rsrc_t &rsrc, int voff, int soff, CK_LDS void *lds_base) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_base);
+    const int so = __builtin_amdgcn_readfirstlane(soff);
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(rsrc), "s"(so)
+                 : "memory", "m0");
+}
+
 // 4-byte global -> LDS DMA (global_load_lds_dword): lane l's word lands at
 // lds_base + 4 * l.
 __device__ __forceinline__ void dma4(const void *g, CK_LDS void *lds_base) {

@@ -210,6 +210,7 @@ __global__ __launch_bounds__(kThreads) void gateup_general_kernel(GemmArgs p) {
 
 // ---- main kernel: 4 waves x (128 x 64 WB), DMA-fed LDS ring ---------------------------
 constexpr int kDThreads = 256;
+constexpr int64_t kMaxDmaK = (int64_t)1 << 21;  // a 256-row operand block stays under 2^31 bytes
 constexpr int kGroupM = 4;   // tile block one XCD runs at once: 4 m-tiles x 8 n-tiles
 constexpr int kGroupN = 8;
 
@@ -292,33 +293,53 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
     const int64_t n0 = (int64_t)ni * kBNhW;
     const int ktiles = (int)(p.k / BK);
 
-    // DMA geometry: instruction j of wave w fills the kRowsPerDma staged rows from
-    // R0 = kRowsPerDma (kD w + j) (waves 0-1: activations, wave 2: gate rows, wave 3:
-    // up rows); lane l -> row R0 + l / (kRB / 16), LDS slot l % (kRB / 16), which holds
-    // global chunk slot ^ f(row): every lane group reads one whole row segment.
+    // DMA geometry: a DMA instruction fills kRowsPerDma consecutive staged rows;
+    // lane l -> row + l / (kRB / 16), LDS slot l % (kRB / 16), which holds global
+    // chunk slot ^ f(row): every lane group reads one whole row segment. DMA j of
+    // wave w: j < kNA -> activation rows from kRowsPerDma (kNA w + j); then kNG
+    // gate-row DMAs and kNG up-row DMAs, each wave a quarter of each block.
+    //   The three operand blocks -- the m-tile's activation rows, the tile's gate
+    // rows, its up rows -- are buffer resources (base and size in SGPRs), and the
+    // block of DMA j is fixed by j alone. A DMA address is a per-lane 32-bit
+    // offset into its block, fixed for the whole loop, plus the K tile's byte
+    // offset in an SGPR: no vector arithmetic per DMA. (A read past a block's size
+    // would return zeros, not fault.)
     constexpr int kLpr = kRB / 16;  // lanes per staged row
-    // Split ring (T::kSplit): DMA j < kD / 2 of wave w fills activation rows from
-    // 8 (kD / 2 w + j), the others weight rows from 8 (kD / 2 w + j - kD / 2), in
-    // the parts of their own operand.
-    const uint16_t *gp[kD];
+    constexpr int kRpd = T::kRowsPerDma;
+    constexpr int kNA = kBM / (kRpd * 4);    // activation DMAs per wave per stage
+    constexpr int kNG = kBNhW / (kRpd * 4);  // gate (and up) DMAs per wave per stage
+    static_assert(kNA + 2 * kNG == kD, "every staged row has one DMA lane group");
+    const int rowb = (int)p.k * 2;  // bytes per operand row (k <= kMaxDmaK)
+    const int a_rows = p.m - m0 < kBM ? (int)(p.m - m0) : kBM;
+    const ck_rsrc_t rsa = buf_rsrc(p.a + m0 * p.k, (uint32_t)(a_rows * rowb));
+    const ck_rsrc_t rsg = buf_rsrc(p.b + n0 * p.k, (uint32_t)(kBNhW * rowb));
+    const ck_rsrc_t rsu = buf_rsrc(p.b + (p.n_half + n0) * p.k, (uint32_t)(kBNhW * rowb));
+    // staged row of DMA j's first row: within the stage, or (split ring) within
+    // its operand's part; and its first row within its operand block
+    auto srow0 = [&](int j) __attribute__((always_inline)) {
+        if (j < kNA) return kRpd * (kNA * wid + j);
+        const int wbase = T::kSplit ? 0 : kBM;
+        if (j < kNA + kNG) return wbase + kRpd * (kNG * wid + j - kNA);
+        return wbase + kBNhW + kRpd * (kNG * wid + j - kNA - kNG);
+    };
+    auto brow0 = [&](int j) __attribute__((always_inline)) {
+        if (j < kNA) return kRpd * (kNA * wid + j);
+        if (j < kNA + kNG) return kRpd * (kNG * wid + j - kNA);
+        return kRpd * (kNG * wid + j - kNA - kNG);
+    };
+    int voff[kD];  // per-lane byte offset of DMA j in its block
 #pragma unroll
     for (int j = 0; j < kD; ++j) {
-        const int R = T::kSplit ? (j < kD / 2 ? 0 : kBM) + 8 * ((kD / 2) * wid + j % (kD / 2)) + lane / kLpr
-                                : T::kRowsPerDma * (kD * wid + j) + lane / kLpr;
-        const int coff = ((lane % kLpr) ^ dsw_swz<BK>(R)) * 8;
-        int64_t grow;
-        const uint16_t *base;
-        if (R < kBM) {
-            grow = m0 + R;
-            if (grow >= p.m) grow = p.m - 1;  // rows past m only feed output rows that are not stored
-            base = p.a;
-        } else {
-            const int wr = R - kBM;
-            grow = wr < kBNhW ? n0 + wr : p.n_half + n0 + (wr - kBNhW);
-            base = p.b;
-        }
-        gp[j] = base + grow * p.k + coff;
+        const int R = srow0(j) + lane / kLpr;  // staged row: its swizzle
+        const int coff = ((lane % kLpr) ^ dsw_swz<BK>(R)) * 16;
+        int row = brow0(j) + lane / kLpr;
+        if (j < kNA && row >= a_rows) row = a_rows - 1;  // rows past m only feed output rows that are not stored
+        voff[j] = row * rowb + coff;
     }
+    // DMA j of K tile `src` into the stage (or part) at `base`
+    auto dma_src = [&](int j, int src, CK_LDS char *base) __attribute__((always_inline)) {
+        dma16_buf(j < kNA ? rsa : j < kNA + kNG ? rsg : rsu, voff[j], src * (BK * 2), base + srow0(j) * kRB);
+    };
     f32x16 acc[4][WB][2];
 #pragma unroll
     for (int ab = 0; ab < 4; ++ab)
@@ -331,8 +352,7 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
 
     // DMA j of this wave: K tile `src` into the ring slot of tile `slot`
     auto dma_one = [&](int slot, int src, int j) {
-        CK_LDS char *dst = smem + (slot % kS) * T::kStageBytes + (kD * wid) * 1024;
-        dma16(gp[j] + (int64_t)src * BK, dst + j * 1024);
+        dma_src(j, src, smem + (slot % kS) * T::kStageBytes);
     };
     // Split ring: part q holds the weights of tile q / 2 (q even) or its
     // activations (q odd) in slot q % 5, so the weight rows of tile t sit in
@@ -340,14 +360,14 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
     auto wslot = [&](int t) { return smem + ((2 * t) % 5) * T::kPart; };
     auto aslot = [&](int t) { return smem + ((2 * t + 1) % 5) * T::kPart; };
     auto dma_w = [&](int t, int src, int jj) {  // weight DMA jj of tile t
-        dma16(gp[kD / 2 + jj] + (int64_t)src * BK, wslot(t) + ((kD / 2) * wid + jj) * 1024);
+        dma_src(kNA + jj, src, wslot(t));
     };
     auto dma_a = [&](int t, int src, int jj) {  // activation DMA jj of tile t
-        dma16(gp[jj] + (int64_t)src * BK, aslot(t) + ((kD / 2) * wid + jj) * 1024);
+        dma_src(jj, src, aslot(t));
     };
     constexpr int kLate = kD - T::kEarlyDma;
     constexpr int kSpE = T::kMfmaSub / T::kEarlyDma > 1 ? T::kMfmaSub / T::kEarlyDma : 1;  // MFMAs per early DMA
-    constexpr int kSpL = kLate > 0 && T::kMfmaSub / kLate > 1 ? T::kMfmaSub / kLate : 1;     // MFMAs per late DMA
+    constexpr int kSpL = T::kMfmaSub / (kLate > 0 ? kLate : 1) > 1 ? T::kMfmaSub / (kLate > 0 ? kLate : 1) : 1;
     static_assert(kLate <= T::kMfmaSub && T::kEarlyDma <= T::kMfmaSub && T::kEarlyDma > 0,
                   "at most one DMA per MFMA");
     // fragment read r of substep s of the tile in ring slot `slot`: r < 2 WB -> weight
@@ -673,7 +693,7 @@ int launch_gemm(const GemmArgs &p, hipStream_t s) {
         CK_RETURN_LAUNCH();
     }
     const int64_t grid = (int64_t)p.mtiles * p.ntiles;
-    if (p.k % 32 == 0) {
+    if (p.k % 32 == 0 && p.k <= kMaxDmaK) {
         // The half-width tile (WB = 1) does about 3/4 of the full tile's work per
         // workgroup (its DMA bytes; half the MFMAs) with twice the workgroups: it
         // wins when it needs fewer than 4/3 as many rounds of resident workgroups
