@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kTW * 64) void stage1_tile_kernel(Stage1Args a) {
     CK_LDS int *s_pages = (CK_LDS int *)(smem + 2 * kTSlots * kTBytes);
 
     const int tid = threadIdx.x;
-    const int wid = tid >> 6;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: DMA LDS addresses in SGPRs
     const int lane = tid & 63;
     const int hh = lane >> 5;
 
@@ -187,29 +187,34 @@ __global__ __launch_bounds__(kTW * 64) void stage1_tile_kernel(Stage1Args a) {
         const int64_t tok0 = (int64_t)(raw < 0 ? 0 : raw) * kPage + (tc & 1) * kTTok;
         return tok0 * head_stride;
     };
+    // a tile's 64 token rows of K or V as a buffer resource (scalar base): the
+    // DMAs add only the fixed lane offsets
+    const uint32_t tile_bytes = (uint32_t)(kTTok * head_stride * 2);
     auto dma_k = [&](int t, int j) {
-        dma16(a.k + tile_src(t) + dma_off[j], kring + (t % kTSlots) * kTBytes + (wid * kTBlk + j) * 1024);
+        dma16_buf(buf_rsrc(a.k + tile_src(t), tile_bytes), (int)(dma_off[j] * 2), 0,
+                  kring + (t % kTSlots) * kTBytes + (wid * kTBlk + j) * 1024);
     };
     auto dma_v = [&](int t, int j) {
-        dma16(a.v + tile_src(t) + dma_off[j], vring + (t % kTSlots) * kTBytes + (wid * kTBlk + j) * 1024);
+        dma16_buf(buf_rsrc(a.v + tile_src(t), tile_bytes), (int)(dma_off[j] * 2), 0,
+                  vring + (t % kTSlots) * kTBytes + (wid * kTBlk + j) * 1024);
     };
     // the iteration-t DMA group: K of tile t + 3 and V of tile t + 2; the two
     // tile bases are looked up once per iteration
     struct DmaGroup {
-        const uint16_t *k, *v;
+        ck_rsrc_t k, v;
         CK_LDS char *kd, *vd;
     };
     auto dma_group = [&](int t) {
         DmaGroup d;
-        d.k = a.k + tile_src(t + 3);
-        d.v = a.v + tile_src(t + 2);
+        d.k = buf_rsrc(a.k + tile_src(t + 3), tile_bytes);
+        d.v = buf_rsrc(a.v + tile_src(t + 2), tile_bytes);
         d.kd = kring + ((t + 3) % kTSlots) * kTBytes + wid * kTBlk * 1024;
         d.vd = vring + ((t + 2) % kTSlots) * kTBytes + wid * kTBlk * 1024;
         return d;
     };
     auto dma_step = [&](const DmaGroup &d, int j) {
-        if (j < kTBlk) dma16(d.k + dma_off[j], d.kd + j * 1024);
-        else dma16(d.v + dma_off[j - kTBlk], d.vd + (j - kTBlk) * 1024);
+        if (j < kTBlk) dma16_buf(d.k, (int)(dma_off[j] * 2), 0, d.kd + j * 1024);
+        else dma16_buf(d.v, (int)(dma_off[j - kTBlk] * 2), 0, d.vd + (j - kTBlk) * 1024);
     };
     auto zero_rows = [&](CK_LDS char *slot, int z0) {
         for (int idx = tid; idx < (kTTok - z0) * 16; idx += kTW * 64) {

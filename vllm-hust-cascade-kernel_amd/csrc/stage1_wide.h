@@ -82,7 +82,7 @@ __device__ __forceinline__ void stage1_wide_body(const Stage1Args &a, CK_LDS cha
     static_assert(NW * 32 * kD * 4 <= SLOTS * kWStage, "epilogue slabs fit the ring");
     CK_LDS int *s_pages = (CK_LDS int *)(smem + SLOTS * kWStage);
 
-    const int wid = tid >> 6;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: DMA LDS addresses in SGPRs
     const int lane = tid & 63;
     const int hh = lane >> 5;
 
@@ -152,15 +152,19 @@ __device__ __forceinline__ void stage1_wide_body(const Stage1Args &a, CK_LDS cha
         const int tt = (wid * kWBlk + j) * 4 + (lane >> 4);
         dma_off[j] = (uint32_t)(tt * head_stride + g * kD + (((lane & 15) ^ tile_swz(tt)) << 3));
     }
-    // DMAs of tile t (t < ntiles) into ring slot t % 4
+    // DMAs of tile t (t < ntiles) into ring slot t % 4: the tile's 64 token rows
+    // of K and of V as buffer resources (scalar base), the lane offsets fixed
+    const uint32_t tile_bytes = (uint32_t)(kTTok * head_stride * 2);
     auto issue = [&](int t) {
         const int raw = __builtin_amdgcn_readfirstlane(s_pages[t >> 1]);
         const int64_t base = ((int64_t)(raw < 0 ? 0 : raw) * kPage + (t & 1) * kTTok) * head_stride;
+        const ck_rsrc_t rk = buf_rsrc(a.k + base, tile_bytes);
+        const ck_rsrc_t rv = buf_rsrc(a.v + base, tile_bytes);
         CK_LDS char *kd = smem + (t % SLOTS) * kWStage + wid * kWBlk * 1024;
 #pragma unroll
         for (int j = 0; j < kWBlk; ++j) {
-            dma16(a.k + base + dma_off[j], kd + j * 1024);
-            dma16(a.v + base + dma_off[j], kd + kTBytes + j * 1024);
+            dma16_buf(rk, (int)(dma_off[j] * 2), 0, kd + j * 1024);
+            dma16_buf(rv, (int)(dma_off[j] * 2), 0, kd + kTBytes + j * 1024);
         }
     };
 
