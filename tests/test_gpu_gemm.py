@@ -66,10 +66,13 @@ def test_swiglu_mode1_small_I(M):
 # (one full-width workgroup) takes the half-width tile, I = 16512 at one m-tile
 # (129 full-width workgroups) the full-width one.
 @pytest.mark.parametrize("I", [128, 16512])
-@pytest.mark.parametrize("K", [64, 96, 128, 160])
+@pytest.mark.parametrize("K", [64, 96, 128, 160, 192, 320])
 def test_swiglu_short_k_ring(K, I):
-    """2-5 K tiles of 32: the DMA ring's prologue and last iterations repeat the
-    last tile into ring slots nothing reads again; the result must not see them."""
+    """1-5 K tiles: K % 64 == 0 runs 64-deep stages (K = 64 .. 320: 1-5 tiles; the
+    full-width tile's five-part ring keeps the weights two tiles ahead), K = 96 and
+    160 run 32-deep stages (3 and 5 tiles). The ring's prologue and last iterations
+    repeat the last tile into parts nothing reads again; the result must not see
+    them. M = 40 leaves 216 activation rows of the m-tile past M."""
     M = 40
     a16, b16 = _inputs(M, K, I, seed=K)
     d, _ = torch.ops.npu.f3_gateup_epilogue(torch_bf16(a16, DEV), torch_bf16(b16, DEV), None, None, 1)
