@@ -357,8 +357,10 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
     // Split ring: part q holds the weights of tile q / 2 (q even) or its
     // activations (q odd) in slot q % 5, so the weight rows of tile t sit in
     // slot 2t % 5 and its activation rows in (2t + 1) % 5.
-    auto wslot = [&](int t) { return smem + ((2 * t) % 5) * T::kPart; };
-    auto aslot = [&](int t) { return smem + ((2 * t + 1) % 5) * T::kPart; };
+    // (the part offsets pass through readfirstlane: they stay one SGPR each instead of
+    // the compiler distributing the modulo over every per-lane read address)
+    auto wslot = [&](int t) { return smem + __builtin_amdgcn_readfirstlane(((2 * t) % 5) * T::kPart); };
+    auto aslot = [&](int t) { return smem + __builtin_amdgcn_readfirstlane(((2 * t + 1) % 5) * T::kPart); };
     auto dma_w = [&](int t, int src, int jj) {  // weight DMA jj of tile t
         dma_src(kNA + jj, src, wslot(t));
     };
@@ -371,18 +373,26 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
     static_assert(kLate <= T::kMfmaSub && T::kEarlyDma <= T::kMfmaSub && T::kEarlyDma > 0,
                   "at most one DMA per MFMA");
     // fragment read r of substep s of the tile in ring slot `slot`: r < 2 WB -> weight
-    // block (gb, gu) = (r >> 1, r & 1), r >= 2 WB -> activation block r - 2 WB
+    // block (gb, gu) = (r >> 1, r & 1), r >= 2 WB -> activation block r - 2 WB. Every
+    // block starts on a multiple of 32 rows, where the row swizzle repeats, so a
+    // read is the slot's (scalar) base + the wave's block offset + an immediate for
+    // the block + lsw[s], the lane's offset of (row l32, chunk 2s + hh) in a block.
+    int lsw[kNS];
+#pragma unroll
+    for (int s = 0; s < kNS; ++s) lsw[s] = dsw_off<BK>(l32, 2 * s + hh);
+    const int woff = ww * 32 * WB * kRB;  // wave-uniform
+    const int aoff = wa * 128 * kRB;
 #define CK_GEMM_READ(slot, s, r, WF, XF)                                                                      \
     do {                                                                                                      \
-        const CK_LDS char *xa_ = T::kSplit ? aslot(slot) : smem + ((slot) % kS) * T::kStageBytes;             \
+        const CK_LDS char *xa_ = T::kSplit ? aslot(slot)                                                      \
+                                           : smem + __builtin_amdgcn_readfirstlane(((slot) % kS) * T::kStageBytes); \
         const CK_LDS char *xw_ = T::kSplit ? wslot(slot) : xa_ + kBM * kRB;                                   \
-        const int ch_ = 2 * (s) + hh;                                                                         \
         if ((r) < 2 * WB)                                                                                     \
             WF[(r) >> 1][(r) & 1] = *reinterpret_cast<const CK_LDS bf16x8 *>(                                  \
-                xw_ + dsw_off<BK>(((r) & 1) * kBNhW + ww * 32 * WB + ((r) >> 1) * 32 + l32, ch_));             \
+                xw_ + woff + (((r) & 1) * kBNhW + ((r) >> 1) * 32) * kRB + lsw[s]);                            \
         else                                                                                                  \
             XF[(r) - 2 * WB] = *reinterpret_cast<const CK_LDS bf16x8 *>(                                      \
-                xa_ + dsw_off<BK>(wa * 128 + ((r) - 2 * WB) * 32 + l32, ch_));                                \
+                xa_ + aoff + ((r) - 2 * WB) * 32 * kRB + lsw[s]);                                             \
     } while (0)
     // Reads in the order the next substep's MFMAs consume them: MFMA 0 needs weight
     // block 0 and activation block 0, then the other weight blocks one per MFMA,
