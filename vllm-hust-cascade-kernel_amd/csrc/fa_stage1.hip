@@ -30,8 +30,9 @@
 //     rows per kv head and enough kv to fill the chip): 8 waves, two per SIMD;
 //     every 64-token K/V tile in LDS feeds 256 rows, and one wave of a SIMD
 //     issues MFMAs while the other waits on reads or runs its softmax.
-//   K/V tiles land by global->LDS DMA (global_load_lds, 16 B per lane; no
-//   staging registers); the split's page ids are read once into LDS, so no
+//   K/V tiles land by buffer->LDS DMA (buffer_load_dwordx4 ... lds, 16 B per
+//   lane, one buffer resource per tile; no staging registers, no vector address
+//   arithmetic); the split's page ids are read once into LDS, so no
 //   load in the loop depends on another load. Q stays in registers as MFMA
 //   operands for the whole kv loop.
 // * S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (A = K rows from LDS, B = Q); the

@@ -25,8 +25,9 @@
 //   (64 gate + 64 up) weight rows, 16 accumulator tiles of 32x32 in the
 //   accumulation registers, so per 16-deep k-substep 8 fragment reads feed 16
 //   MFMAs (half an LDS read per MFMA). Operand tiles stream global -> LDS by
-//   DMA (global_load_lds_dwordx4: no staging registers, no LDS write
-//   instructions). With K a multiple of 64 a stage is 64 deep, so each staged
+//   DMA (buffer_load_dwordx4 ... lds on per-block buffer resources: no staging
+//   registers, no LDS write instructions, no vector address arithmetic). With K
+//   a multiple of 64 a stage is 64 deep, so each staged
 //   row is one whole 128-byte line and a DMA instruction fetches 8 whole lines
 //   (with 32-deep stages it fetched 16 half lines: the address unit's cost per
 //   byte doubles, and it bounded the kernel). Two such 64-KB stages would fill
