@@ -57,8 +57,9 @@ __device__ __forceinline__ void dma16(const void *g, CK_LDS void *lds_base) {
 }
 
 // A raw buffer resource (V#) for `bytes` bytes from `base`: the 4 dwords
-// buffer_load takes in SGPRs (wave-uniform by construction). Reads past
-// `bytes` return zeros.
+// buffer_load takes in SGPRs (wave-uniform by construction). A lane whose
+// per-lane offset is at or past `bytes` reads zeros (the scalar offset is not
+// range-checked).
 typedef int ck_rsrc_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ ck_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
     const uint64_t a = (uint64_t)(uintptr_t)base;

@@ -303,8 +303,8 @@ __global__ __launch_bounds__(kDThreads, 1) void gateup_dma_kernel(GemmArgs p) {
     // rows, its up rows -- are buffer resources (base and size in SGPRs), and the
     // block of DMA j is fixed by j alone. A DMA address is a per-lane 32-bit
     // offset into its block, fixed for the whole loop, plus the K tile's byte
-    // offset in an SGPR: no vector arithmetic per DMA. (A read past a block's size
-    // would return zeros, not fault.)
+    // offset in an SGPR: no vector arithmetic per DMA. Every offset stays inside its
+    // block: the lane offset within the block's rows, the K tile offset within a row.
     constexpr int kLpr = kRB / 16;  // lanes per staged row
     constexpr int kRpd = T::kRowsPerDma;
     constexpr int kNA = kBM / (kRpd * 4);    // activation DMAs per wave per stage
