@@ -1,6 +1,7 @@
 """Benchmark of the cascade-decode operator set on one MI355X.
 
-The step (timed exactly --steps times after --warmup untimed steps) is one fused
+The step (timed exactly --steps times after --warmup untimed steps, which follow
+--settle-ms of untimed steps that bring the clocks to their sustained state) is one fused
 npu.cascade_decode call at BASELINE config 2's attention shapes, end to end:
   32 query heads, 8 kv heads, head dim 128, bf16; a shared 8192-token prefix (64
   pages of 128 tokens, permuted physical pages) read by stage-1 in the flattened
@@ -56,6 +57,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--settle-ms", type=float, default=100.0,
+                    help="untimed steps run back to back for this long before the warm-up steps, "
+                         "so the GPU clocks reach their sustained state")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="only the step loop and the cascade's ops")
     return ap.parse_args()
@@ -201,6 +205,18 @@ def main():
         q, k, v = c["pools"][i % c["copies"]]
         return torch.ops.npu.cascade_decode(q, k, v, c["bt_pre"], c["kvlens"], k, v, c["bt_suf"], c["suf"])
 
+    # Clock settle: from idle the GPU needs some tens of ms of sustained load before
+    # its clocks stop ramping (20-step windows of this step measured 57-61 us from a
+    # cold start and a steady 54 us after ~20 ms); then the --warmup steps and the
+    # timed steps follow without a pause.
+    settle_steps = 0
+    t_settle = time.perf_counter()
+    while (time.perf_counter() - t_settle) * 1e3 < args.settle_ms:
+        for _ in range(50):
+            cascade(settle_steps)
+            settle_steps += 1
+        torch.cuda.synchronize()
+    settle_ms = (time.perf_counter() - t_settle) * 1e3
     for i in range(args.warmup):
         cascade(i)
     torch.cuda.synchronize()
@@ -262,6 +278,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"steps": settle_steps, "ms": round(settle_ms, 1)},
         "ms_per_step": round(ms_step, 5),
         "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
         "higher_is_better": True,
