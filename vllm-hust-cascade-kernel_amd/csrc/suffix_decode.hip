@@ -252,16 +252,16 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
                                            false);
 }
-// 16-dim bf16 dot product (two 8-dim halves, two chains)
+// 16-dim bf16 dot product: one chain of 8 (the callers interleave one chain per
+// query head, which covers the chain's latency; two chains per head cost a
+// second zero-initialised accumulator and an add)
 __device__ __forceinline__ float dot16(const u32x4 &k0, const u32x4 &k1, const u32x4 &q0, const u32x4 &q1) {
-    float d0 = dot2(k0[0], q0[0], 0.f), d1 = dot2(k1[0], q1[0], 0.f);
-    d0 = dot2(k0[1], q0[1], d0);
-    d1 = dot2(k1[1], q1[1], d1);
-    d0 = dot2(k0[2], q0[2], d0);
-    d1 = dot2(k1[2], q1[2], d1);
-    d0 = dot2(k0[3], q0[3], d0);
-    d1 = dot2(k1[3], q1[3], d1);
-    return d0 + d1;
+    float d = dot2(k0[0], q0[0], 0.f);
+#pragma unroll
+    for (int i = 1; i < 4; ++i) d = dot2(k0[i], q0[i], d);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d = dot2(k1[i], q1[i], d);
+    return d;
 }
 
 __device__ __forceinline__ int64_t clamp_len(const SuffixArgs &a, int64_t kvl) {
@@ -442,6 +442,28 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                 vv[j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)ov, 0, 0));
             }
         }
+    };
+
+    // Token-major windows issue their K and V halves at different points of a step
+    // (K before the scores, V after the values of the window whose slot it reuses);
+    // both halves address the same rows through the same per-lane offset.
+    struct TokWin {
+        int64_t off;
+        int range;
+        uint32_t o;
+    };
+    auto tok_win = [&](i32x2 e) __attribute__((always_inline)) {
+        const int page = __builtin_amdgcn_readfirstlane(e[0]);
+        const int ey = __builtin_amdgcn_readfirstlane(e[1]);
+        const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
+        return TokWin{(int64_t)(page < 0 ? 0 : page) * pgb + (int64_t)(tab_sub(ey) * kWin) * tokb,
+                      page < 0 ? 0 : (int)win_bytes, t < t1 ? koff : kOob};
+    };
+    auto issue_half = [&](const char *base, const TokWin &w, u32x4 &x0, u32x4 &x1) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t r =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base + w.off), (short)0, w.range, kRsrcFlags);
+        x0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)w.o, 0, 0));
+        x1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(w.o + 128), 0, 0));
     };
 
     // Closes segment b (sequence b's windows in this range): folds the lanes' partial
@@ -670,17 +692,17 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
       }
     };
 
-    // Token-major window step, pipelined by one window: step n issues window
-    // n + D, computes the scores of window n and the values of window n - 1 (its p
-    // and V rows kept from the step before) -- two independent chains in one basic
-    // block, so each fills the other's latencies -- then closes window n - 1's
-    // segment if it ends there and finishes window n's softmax. The table entry of
-    // the window to issue was read one step ahead and the packed fields of each
-    // window travel in the ring with its data, so the step's only LDS access is
-    // off its critical path.
+    // Token-major window step, pipelined by one window: step n issues the K rows of
+    // window n + D, computes the scores of window n and the values of window n - 1
+    // (its p kept from the step before, its V rows still in their ring slot) -- two
+    // independent chains in one basic block, so each fills the other's latencies --
+    // then issues window n + D's V rows into the slot window n - 1's values just
+    // left, closes window n - 1's segment if it ends there and finishes window n's
+    // softmax. The table entry of the window to issue was read one step ahead and
+    // the packed fields of each window travel in the ring with its data, so the
+    // step's only LDS access is off its critical path.
     i32x2 enext = i32x2{-1, 0};
     float pp[G];     // p of window n - 1 (0 before a phase's first window)
-    VSlot vpend;     // V rows of window n - 1
     int eypend = 0;  // packed table fields of window n - 1
     auto pv_tok = [&](const float *p, const VSlot &vv) __attribute__((always_inline)) {
         if constexpr (TOK) {
@@ -703,9 +725,10 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     auto step_tok = [&](auto jc, int n, int np) __attribute__((always_inline)) {
       if constexpr (TOK) {
         constexpr int J = decltype(jc)::value;
-        constexpr int JI = (J + D) % NB;  // window n + D, into the slot window n - 1 freed
+        constexpr int JI = (J + D) % NB;  // window n + D, into the slot of window n - 1
         const i32x2 ei = enext;
-        issue(ei, kbuf[JI][0], kbuf[JI][1], vbuf[JI]);
+        const TokWin wi = tok_win(ei);
+        issue_half(kbase, wi, kbuf[JI][0], kbuf[JI][1]);
         const int ey = eyr[J];
         const int eyp = eypend;
         eyr[JI] = __builtin_amdgcn_readfirstlane(ei[1]);
@@ -728,10 +751,9 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
 #pragma unroll
             for (int h = 0; h < G; ++h) s[h] = sum8(dot16(k0, k1, qr[h][0], qr[h][1])) * a.scale_log2;
         }
-        pv_tok(pp, vpend);
+        pv_tok(pp, vbuf[JI]);
+        if constexpr (TOK) issue_half(vbase, wi, vbuf[JI][0], vbuf[JI][1]);
         if (tab_last(eyp)) close_seg(tab_b(eyp));
-        vpend[0] = vbuf[J][0];
-        vpend[1] = vbuf[J][1];
         eypend = ey;
         if (tab_first(ey)) {
 #pragma unroll
@@ -769,10 +791,14 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         }
       }
     };
-    // after a phase's last window: its values and its segment's close
-    auto drain_tok = [&]() __attribute__((always_inline)) {
+    // after a phase's last window (np - 1, in slot (np - 1) % NB): its values and
+    // its segment's close
+    auto drain_tok = [&](int np) __attribute__((always_inline)) {
       if constexpr (TOK) {
-        pv_tok(pp, vpend);
+        const int js = (np - 1) % NB;  // wave-uniform
+        static_for<NB>([&](auto jc) __attribute__((always_inline)) {
+            if (js == decltype(jc)::value) pv_tok(pp, vbuf[decltype(jc)::value]);
+        });
         if (tab_last(eypend)) close_seg(tab_b(eypend));
       }
     };
@@ -845,11 +871,12 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         }
         if constexpr (TOK) {
             enext = D < np ? tab[D] : i32x2{-1, 0};
-            // "window -1" of the pipelined step: no values, no close
+            // "window -1" of the pipelined step (slot NB - 1): no values, no close;
+            // its V slot is zeroed so that p = 0 times it stays 0
 #pragma unroll
             for (int h = 0; h < G; ++h) pp[h] = 0.f;
-            vpend[0] = u32x4{0u, 0u, 0u, 0u};
-            vpend[1] = u32x4{0u, 0u, 0u, 0u};
+            vbuf[NB - 1][0] = u32x4{0u, 0u, 0u, 0u};
+            vbuf[NB - 1][1] = u32x4{0u, 0u, 0u, 0u};
             eypend = 0;
         }
         // full rounds of NB steps, then the rest: the ring slot of every step is a
@@ -870,7 +897,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                 else step(jc, n + decltype(jc)::value, np);
             }
         });
-        drain_tok();
+        drain_tok(np);
         p0 = p1;
     }
 }
