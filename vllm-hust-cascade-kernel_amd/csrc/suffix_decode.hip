@@ -411,7 +411,11 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     u32x4 kbuf[NB][2];
     using VSlot = std::conditional_t<TOK, u32x4[2], u32x2[4]>;
     VSlot vbuf[NB];
-    u32x4 qr[TOK ? G : 1][2];  // token-major: this lane's 16 q dims of each head
+    // q in registers from the window that opens a segment: the token-major body,
+    // and the stand-alone dims-major body above 4 heads (one workgroup per CU, so
+    // the 8 G registers cost no occupancy); else q is read from LDS per window
+    constexpr bool kQReg = TOK || (G > 4 && NW == kWaves);
+    u32x4 qr[kQReg ? G : 1][2];  // this lane's 16 q dims of each head
     int eyr[NB];               // token-major: packed table fields of the window in each slot
     constexpr int kPwRow = (G + 3) / 4 * 4;  // floats per token in this wave's p rows
     static_assert(kPwRow <= 8, "p row");
@@ -616,6 +620,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         const int ey = __builtin_amdgcn_readfirstlane(tab[n][1]);
         const int b = tab_b(ey);
         const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
+        const CK_LDS char *qrow = qs + qslot * G * (kD * 2) + c * 16;
         if (tab_first(ey)) {
 #pragma unroll
             for (int h = 0; h < G; ++h) {
@@ -623,18 +628,25 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                 l[h] = 0.f;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[h][e] = 0.f;
+                if constexpr (kQReg) {
+                    qr[h][0] = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2));
+                    qr[h][1] = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2) + 128);
+                }
             }
         }
         if (t1 > 0) {
-            const CK_LDS char *qrow = qs + qslot * G * (kD * 2) + c * 16;
             const u32x4 k0 = kbuf[J][0], k1 = kbuf[J][1];
             float s[G];  // scores, then p in place
             bool trig = false;
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                const u32x4 q0 = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2));
-                const u32x4 q1 = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2) + 128);
-                s[h] = sum8(dot16(k0, k1, q0, q1)) * a.scale_log2;
+                if constexpr (kQReg) {
+                    s[h] = sum8(dot16(k0, k1, qr[h][0], qr[h][1])) * a.scale_log2;
+                } else {
+                    const u32x4 q0 = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2));
+                    const u32x4 q1 = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2) + 128);
+                    s[h] = sum8(dot16(k0, k1, q0, q1)) * a.scale_log2;
+                }
             }
             if (t1 < 8) {
 #pragma unroll
