@@ -46,7 +46,7 @@ NORM_M, NORM_K = 2048, 5120  # add_rms_norm_stats at the reference's prefill-mai
 ROTATE_BYTES = 2 << 30
 # the kernels each op launches (an op's HIP-event time covers all of them)
 OP_KERNELS = {"cascade_decode": "cascade_fused_kernel + cascade_epilogue_kernel",
-              "fa_fp32_stage1": "stage1_kernel + stage1_combine_kernel",
+              "fa_fp32_stage1": "stage1_narrow_kernel + stage1_combine_kernel",
               "suffix_decode": "suffix_stream_kernel + suffix_fixup_kernel",
               "lse_merge": "lse_merge_kernel"}
 CPU_THREADS_MAX = 16         # the GPU box's host-core share for one GPU

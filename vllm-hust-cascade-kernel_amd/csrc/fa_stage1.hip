@@ -20,12 +20,11 @@
 // * Every wave owns 32 query rows and all tokens of them, so a row has one
 //   online-softmax state over the whole split and P is rounded on the row's
 //   own running maximum (moved once per 64-token tile; for kv <= 64 that is
-//   the row maximum the reference rounds on). Two kernels:
-//   - stage1_tile_kernel (m-tile of 128 rows): 4 waves, one per SIMD with 512
-//     registers. Iteration t runs the QK MFMAs of tile t + 1 and the PV MFMAs
-//     of tile t in a fixed issue order, with one slice of tile t's softmax
-//     and, every four MFMAs, one of the wave's DMAs between them. K and V
-//     stream through separate 3-slot LDS rings (K one tile ahead of V).
+//   the row maximum the reference rounds on). Two kernels run the same body
+//   (stage1_wide.h):
+//   - stage1_narrow_kernel (m-tile of 128 rows): 4 waves with at most 256
+//     registers each and a 3-slot K/V ring, the body the fused cascade kernel
+//     runs as its stage-1 role.
 //   - stage1_wide_kernel (m-tile of 256 rows, when a request has more than 128
 //     rows per kv head and enough kv to fill the chip): 8 waves, two per SIMD;
 //     every 64-token K/V tile in LDS feeds 256 rows, and one wave of a SIMD
@@ -67,482 +66,17 @@ namespace {
 
 using namespace s1;
 
-// Software-pipelined whole-row kernel. 4 waves (one per SIMD, 512 registers
-// each); wave w owns RB blocks of 32 query rows (rows 32 RB w .. + 32 RB of the
-// workgroup's 128 RB) and every token of them, so each row has one
-// online-softmax state and P is rounded on the row's own running maximum,
-// which moves once per 64-token tile. Every K or V fragment read from LDS
-// feeds RB MFMAs (RB = 2 halves the LDS bytes per MFMA).
-// Iteration t runs the QK MFMAs of tile t + 1 and the PV MFMAs of tile t in a
-// fixed order, with one slice of tile t's softmax and, every few MFMAs, one of
-// the wave's 8 DMAs of the tile two ahead between them: the wave issues its
-// VALU work and DMAs while the matrix pipe is busy. K and V stream through
-// separate 3-slot LDS rings (K is read one iteration before V), so every DMA
-// is issued two iterations before its first reader. Past the last tile the
-// DMAs repeat into slots nobody reads again, so every iteration issues the
-// same number and the vmcnt wait is exact.
-constexpr int kTW = 4;                               // waves per workgroup
-constexpr int kTSlots = 3;                           // ring depth of each of K and V
-constexpr int kTBlk = kTBytes / 1024 / kTW;          // 1-KB DMAs of K (and of V) per wave per tile
-constexpr int kTDma = 2 * kTBlk;                     // DMAs per wave per tile
-constexpr int kTLds = 2 * kTSlots * kTBytes + kMaxSplitPages * 4;
-
-template <int RB>
-__global__ __launch_bounds__(kTW * 64) void stage1_tile_kernel(Stage1Args a) {
-    constexpr int kRowsWg = kTW * 32 * RB;
-    // the epilogue parks every row block's 16 KB of O in the (idle) rings; RB = 2
-    // would also need more than a wave's 512 registers (it spills), so the
-    // launcher instantiates RB = 1 only
-    static_assert(kTW * RB * 32 * kD * 4 <= 2 * kTSlots * kTBytes, "epilogue slabs fit the rings");
-    extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-    CK_LDS char *smem = (CK_LDS char *)smem_raw;
-    CK_LDS char *kring = smem;
-    CK_LDS char *vring = smem + kTSlots * kTBytes;
-    CK_LDS int *s_pages = (CK_LDS int *)(smem + 2 * kTSlots * kTBytes);
-
-    const int tid = threadIdx.x;
-    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: DMA LDS addresses in SGPRs
-    const int lane = tid & 63;
-    const int hh = lane >> 5;
-
-    uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
-    const int mt = w % a.mtiles;
-    w /= a.mtiles;
-    const int sp = w % a.num_splits;
-    w /= a.num_splits;
-    const int g = w % a.kv_heads;
-    const int b = w / a.kv_heads;
-
-    int qlen, qs;
-    if (a.q_len_uniform > 0) {
-        qlen = a.q_len_uniform;
-        qs = b * qlen;
-    } else {
-        qlen = (int)a.q_seqlens[b];
-        qs = a.q_start[b];
-    }
-    const int rows_b = qlen * a.group;
-    const int row0 = mt * kRowsWg;
-    if (row0 >= rows_b) return;  // uniform over the workgroup
-
-    const int wrow0 = row0 + wid * 32 * RB;
-    const bool wave_active = wrow0 < rows_b;
-    int64_t qrow[RB];
-    bool row_valid[RB];
-    bf16x8 qf[RB][8];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-        const int r = wrow0 + rb * 32 + (lane & 31);
-        row_valid[rb] = r < rows_b;
-        const int t_local = r / a.group;
-        const int h = g * a.group + (r - t_local * a.group);
-        qrow[rb] = (int64_t)(qs + t_local) * a.num_heads + h;
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-            if (row_valid[rb]) {
-                qf[rb][kk] = *reinterpret_cast<const bf16x8 *>(a.q + qrow[rb] * kD + 16 * kk + 8 * hh);
-            } else {
-                qf[rb][kk] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
-            }
-        }
-    }
-    const int kv_lo = sp * a.split_len;  // a multiple of the page size
-    {
-        const int pg0 = kv_lo / kPage;
-        const int64_t avail = a.bt_cols - pg0;
-        const int pg_n = (int)min((int64_t)(a.split_len / kPage), avail > 0 ? avail : (int64_t)0);
-        for (int pi = tid; pi < pg_n; pi += kTW * 64) {
-            const int page = a.bt[(int64_t)b * a.bt_cols + pg0 + pi];
-            s_pages[pi] = (page >= 0 && (int64_t)page < a.num_blocks) ? page : -1;
-        }
-    }
-    int64_t kvl = a.kv_seqlens[b];
-    const int64_t kv_lim = a.bt_cols * kPage;
-    if (kvl > kv_lim) kvl = kv_lim;
-    if (kvl > a.kv_cap) kvl = a.kv_cap;
-    if (kvl < 0 || a.num_blocks <= 0) kvl = 0;
-    int kv_hi = kv_lo + a.split_len;
-    if (kv_hi > (int)kvl) kv_hi = (int)kvl;
-    const int ntok = kv_hi > kv_lo ? kv_hi - kv_lo : 0;
-    const int ntiles = (ntok + kTTok - 1) / kTTok;
-
-    wait_vmcnt<0>();
-    __syncthreads();  // s_pages visible
-
-    // DMA geometry: one wave instruction moves 4 token rows (1 KB); lane ->
-    // token 4 blk + lane / 16 and LDS chunk lane % 16, which holds global chunk
-    // (lane % 16) ^ tile_swz(token). Per-lane element offsets inside a tile.
-    const int64_t head_stride = (int64_t)a.kv_heads * kD;
-    uint32_t dma_off[kTBlk];
-#pragma unroll
-    for (int j = 0; j < kTBlk; ++j) {
-        const int tt = (wid * kTBlk + j) * 4 + (lane >> 4);
-        dma_off[j] = (uint32_t)(tt * head_stride + g * kD + (((lane & 15) ^ tile_swz(tt)) << 3));
-    }
-    // DMA j (0 .. kTDma-1: K blocks, then V blocks) of the wave's share of tile
-    // t (K) or tile t - 1 (V) -- the two the iteration before t prefetches. A
-    // tile past the end repeats the last tile into its own (dead) slot.
-    auto tile_src = [&](int t) {  // called only when ntiles > 0
-        const int tc = t < ntiles ? t : ntiles - 1;
-        const int raw = __builtin_amdgcn_readfirstlane(s_pages[tc >> 1]);
-        const int64_t tok0 = (int64_t)(raw < 0 ? 0 : raw) * kPage + (tc & 1) * kTTok;
-        return tok0 * head_stride;
-    };
-    // a tile's 64 token rows of K or V as a buffer resource (scalar base): the
-    // DMAs add only the fixed lane offsets
-    const uint32_t tile_bytes = (uint32_t)(kTTok * head_stride * 2);
-    auto dma_k = [&](int t, int j) {
-        dma16_buf(buf_rsrc(a.k + tile_src(t), tile_bytes), (int)(dma_off[j] * 2), 0,
-                  kring + (t % kTSlots) * kTBytes + (wid * kTBlk + j) * 1024);
-    };
-    auto dma_v = [&](int t, int j) {
-        dma16_buf(buf_rsrc(a.v + tile_src(t), tile_bytes), (int)(dma_off[j] * 2), 0,
-                  vring + (t % kTSlots) * kTBytes + (wid * kTBlk + j) * 1024);
-    };
-    // the iteration-t DMA group: K of tile t + 3 and V of tile t + 2; the two
-    // tile bases are looked up once per iteration
-    struct DmaGroup {
-        ck_rsrc_t k, v;
-        CK_LDS char *kd, *vd;
-    };
-    auto dma_group = [&](int t) {
-        DmaGroup d;
-        d.k = buf_rsrc(a.k + tile_src(t + 3), tile_bytes);
-        d.v = buf_rsrc(a.v + tile_src(t + 2), tile_bytes);
-        d.kd = kring + ((t + 3) % kTSlots) * kTBytes + wid * kTBlk * 1024;
-        d.vd = vring + ((t + 2) % kTSlots) * kTBytes + wid * kTBlk * 1024;
-        return d;
-    };
-    auto dma_step = [&](const DmaGroup &d, int j) {
-        if (j < kTBlk) dma16_buf(d.k, (int)(dma_off[j] * 2), 0, d.kd + j * 1024);
-        else dma16_buf(d.v, (int)(dma_off[j - kTBlk] * 2), 0, d.vd + (j - kTBlk) * 1024);
-    };
-    auto zero_rows = [&](CK_LDS char *slot, int z0) {
-        for (int idx = tid; idx < (kTTok - z0) * 16; idx += kTW * 64) {
-            const int tt = z0 + (idx >> 4), c = idx & 15;
-            *reinterpret_cast<CK_LDS u32x4 *>(slot + tt * 256 + c * 16) = u32x4{0, 0, 0, 0};
-        }
-    };
-    auto page_ok = [&](int t) { return s_pages[t >> 1] >= 0; };
-
-    f32x16 oacc[RB][4];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) oacc[rb][db][i] = 0.f;
-    float m_run[RB], l_part[RB];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-        m_run[rb] = -INFINITY;
-        l_part[rb] = 0.f;
-    }
-
-    const int trG = (lane >> 4) & 3;
-    const int tr_row = (lane & 15) >> 2;
-    const int tr_e4 = lane & 3;
-    const int ktok = lane & 31;
-    auto vt_off = [&](int s16, int db, int second) {
-        const int t1 = 16 * s16 + 4 * (trG >> 1) + tr_row + 8 * second;
-        const int d = 32 * db + 16 * (trG & 1) + 4 * tr_e4;
-        return tile_off(t1, d >> 3) + (d & 7) * 2;
-    };
-    // K fragment f of a tile (f = 2 kk + q2: 16-dim step kk of token block q2)
-    auto kfrag = [&](const CK_LDS char *kb, int f) {
-        return *reinterpret_cast<const CK_LDS bf16x8 *>(kb + tile_off(32 * (f & 1) + ktok, 2 * (f >> 1) + hh));
-    };
-    // S^T of the tile in `kb` without interleaving (prologue)
-    auto qk_tile = [&](const CK_LDS char *kb, f32x16 (*sb)[2]) {
-        const f32x16 zero16 = {};
-#pragma unroll
-        for (int f = 0; f < 16; ++f) {
-            const bf16x8 kf = kfrag(kb, f);
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb)
-                sb[rb][f & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[rb][f >> 1],
-                                                                        f < 2 ? zero16 : sb[rb][f & 1], 0, 0, 0);
-        }
-    };
-
-    // ---- per-tile softmax pieces (p replaces s in place; P packed per 16 tokens) ----
-    // group s16 of row block rb: elements 8 (s16 & 1) .. + 8 of token block s16 / 2
-    float smax[RB], m_use[RB], dmv[RB], lsum[RB];
-    bool rescale = false;
-    auto soft_begin = [&]() {
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            smax[rb] = -INFINITY;
-            lsum[rb] = 0.f;
-        }
-    };
-    auto max_chunk = [&](f32x16 (*sc)[2], int c) {  // c < 4 RB: 8 scores
-        const int rb = c >> 2, q2 = (c >> 1) & 1, e0 = 8 * (c & 1);
-#pragma unroll
-        for (int e = e0; e < e0 + 8; ++e) smax[rb] = fmaxf(smax[rb], sc[rb][q2][e]);
-    };
-    auto max_finish = [&]() {
-        bool any = false;
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            const float mx = max_xor32(smax[rb]) * a.scale_log2;
-            const float m_new = fmaxf(m_run[rb], mx);
-            m_use[rb] = (m_new == -INFINITY) ? 0.f : m_new;
-            dmv[rb] = exp2_fast(m_run[rb] - m_use[rb]);
-            m_run[rb] = m_new;
-            any |= dmv[rb] != 1.0f;
-        }
-        // O moves only when some row's max moved (wave-uniform)
-        rescale = __builtin_amdgcn_ballot_w64(any) != 0;
-    };
-    auto rescale_chunk = [&](int c) {  // c < 4 RB: 16 accumulators
-        if (rescale) {
-            const int rb = c >> 2, db = c & 3;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) oacc[rb][db][e] *= dmv[rb];
-        }
-    };
-    bf16x8 pbv[4][RB];
-    auto exp_chunk = [&](f32x16 (*sc)[2], int s16, int rb, int hf) {  // 4 scores; hf 1 packs the group
-        const int q2 = s16 >> 1, e0 = 8 * (s16 & 1) + 4 * hf;
-#pragma unroll
-        for (int e = e0; e < e0 + 4; ++e) {
-            const float pv = exp2_fast(fmaf(sc[rb][q2][e], a.scale_log2, -m_use[rb]));
-            sc[rb][q2][e] = pv;
-            lsum[rb] += pv;
-        }
-        if (hf == 1) pbv[s16][rb] = pack_p(sc[rb][q2], 8 * (s16 & 1));
-    };
-    auto soft_end = [&]() {
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) l_part[rb] = l_part[rb] * dmv[rb] + lsum[rb];
-    };
-
-    // One full tile of the main loop (t + 1 < ntiles): a fixed issue order, one
-    // step per MFMA, fenced so the compiler keeps it.
-    //   QK of tile t + 1 (16 RB MFMAs, K fragments read four ahead) with tile t's
-    //   row max, step factors, O rescale and the exp of its 16-token groups 0-1;
-    //   PV of tile t (16 RB MFMAs, V^T fragments read two 4-fragment groups
-    //   ahead) with the exp of groups 2-3; a DMA every 4 RB MFMAs.
-    constexpr int kNQ = 16 * RB;
-    auto tile_body = [&](int t, f32x16 (*sc)[2], f32x16 (*sn)[2]) {
-        const CK_LDS char *kb = kring + ((t + 1) % kTSlots) * kTBytes;
-        const CK_LDS char *vb = vring + (t % kTSlots) * kTBytes;
-        const f32x16 zero16 = {};
-        const DmaGroup dg = dma_group(t);
-        soft_begin();
-        bf16x8 kfr[4];
-#pragma unroll
-        for (int f = 0; f < 4; ++f) kfr[f] = kfrag(kb, f);
-#pragma unroll
-        for (int i = 0; i < kNQ; ++i) {
-            const int f = i / RB, rb = i % RB;
-            sn[rb][f & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[f & 3], qf[rb][f >> 1],
-                                                                    f < 2 ? zero16 : sn[rb][f & 1], 0, 0, 0);
-            if (rb == RB - 1 && f + 4 < 16) kfr[f & 3] = kfrag(kb, f + 4);
-            // softmax slice: 4 RB max chunks, 4 RB rescale chunks, then the 4 RB exp
-            // chunks of groups 0-1 (2 RB per group: row block, half)
-            const int c = i;
-            if (c < 4 * RB) {
-                max_chunk(sc, c);
-                if (c == 4 * RB - 1) max_finish();
-            } else if (c < 8 * RB) {
-                rescale_chunk(c - 4 * RB);
-            } else if (c < 12 * RB) {
-                const int x = c - 8 * RB;
-                exp_chunk(sc, x / (2 * RB), (x / 2) % RB, x & 1);
-            }
-            if (i % (kNQ / (kTDma / 2)) == kNQ / (kTDma / 2) - 1) dma_step(dg, i / (kNQ / (kTDma / 2)));
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        uint2 vlo[3][4], vhi[3][4];
-#pragma unroll
-        for (int s0 = 0; s0 < 2; ++s0)
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                vlo[s0][db] = lds_read_tr16(vb + vt_off(s0, db, 0));
-                vhi[s0][db] = lds_read_tr16(vb + vt_off(s0, db, 1));
-            }
-#pragma unroll
-        for (int i = 0; i < kNQ; ++i) {
-            const int fv = i / RB, rb = i % RB, s16 = fv >> 2, db = fv & 3, bsel = s16 % 3;
-            const bf16x8 vf = __builtin_bit_cast(
-                bf16x8, make_uint4(vlo[bsel][db].x, vlo[bsel][db].y, vhi[bsel][db].x, vhi[bsel][db].y));
-            oacc[rb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pbv[s16][rb], oacc[rb][db], 0, 0, 0);
-            if (rb == RB - 1 && s16 + 2 < 4) {
-                vlo[(s16 + 2) % 3][db] = lds_read_tr16(vb + vt_off(s16 + 2, db, 0));
-                vhi[(s16 + 2) % 3][db] = lds_read_tr16(vb + vt_off(s16 + 2, db, 1));
-            }
-            // exp of groups 2-3 (2 RB chunks each) over the first PV steps, each
-            // group finished before its first MFMA (group 2 at step 8 RB)
-            if (i < 4 * RB) exp_chunk(sc, 2 + i / (2 * RB), (i / 2) % RB, i & 1);
-            if (i % (kNQ / (kTDma / 2)) == kNQ / (kTDma / 2) - 1)
-                dma_step(dg, kTDma / 2 + i / (kNQ / (kTDma / 2)));
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        soft_end();
-    };
-
-    f32x16 s_a[RB][2], s_b[RB][2];
-    // prologue: K of tiles 0-2 and V of tiles 0-1 in flight (repeats past the
-    // end). A split with no tokens (a request shorter than the split's start)
-    // issues nothing: every DMA source is a tile index clamped to ntiles - 1.
-    if (ntiles > 0) {
-#pragma unroll
-        for (int j = 0; j < kTBlk; ++j) {
-            dma_k(0, j);
-            dma_k(1, j);
-            dma_k(2, j);
-            dma_v(0, j);
-            dma_v(1, j);
-        }
-    }
-    wait_vmcnt<0>();
-    __syncthreads();
-    if (ntiles > 0 && !page_ok(0)) {
-        zero_rows(kring, 0);
-        __syncthreads();
-    }
-    if (ntiles > 0 && wave_active) qk_tile(kring, s_a);
-
-    // every tile but the last is full (64 tokens)
-    auto tile_top = [&](int t) {
-        // this iteration reads K of tile t + 1 and V of tile t (issued two
-        // iterations ago); the previous iteration's group may stay in flight
-        wait_vmcnt<kTDma>();
-        __syncthreads();  // ... for every wave; and every wave is done with tile t - 1
-        const bool v_fill = !page_ok(t);
-        const bool k_fill = !page_ok(t + 1);
-        if (v_fill) zero_rows(vring + (t % kTSlots) * kTBytes, 0);
-        if (k_fill) zero_rows(kring + ((t + 1) % kTSlots) * kTBytes, 0);
-        if (v_fill || k_fill) __syncthreads();
-    };
-    auto idle_dmas = [&](int t) {
-        const DmaGroup dg = dma_group(t);
-#pragma unroll
-        for (int j = 0; j < kTDma; ++j) dma_step(dg, j);
-    };
-    int t = 0;
-    for (; t + 2 < ntiles; t += 2) {
-        tile_top(t);
-        if (wave_active) tile_body(t, s_a, s_b);
-        else idle_dmas(t);
-        tile_top(t + 1);
-        if (wave_active) tile_body(t + 1, s_b, s_a);
-        else idle_dmas(t + 1);
-    }
-    if (t + 1 < ntiles) {
-        tile_top(t);
-        if (wave_active) {
-            tile_body(t, s_a, s_b);
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb) {
-                s_a[rb][0] = s_b[rb][0];
-                s_a[rb][1] = s_b[rb][1];
-            }
-        } else {
-            idle_dmas(t);
-        }
-        ++t;
-    }
-    // the last tile: tokens past the split's end are masked (p = 0) and their V
-    // rows zeroed, so 0 * V cannot produce a NaN from rows nobody wrote
-    if (ntiles > 0) {
-        wait_vmcnt<0>();
-        __syncthreads();
-        const int nv = ntok - t * kTTok;
-        if (nv < kTTok || !page_ok(t)) {
-            zero_rows(vring + (t % kTSlots) * kTBytes, page_ok(t) ? nv : 0);
-            __syncthreads();
-        }
-        if (wave_active) {
-            if (nv < kTTok) {
-#pragma unroll
-                for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-                    for (int q2 = 0; q2 < 2; ++q2)
-#pragma unroll
-                        for (int e = 0; e < 16; ++e) {
-                            const int tok = 32 * q2 + (e & 3) + 8 * (e >> 2) + 4 * hh;
-                            if (tok >= nv) s_a[rb][q2][e] = -INFINITY;
-                        }
-            }
-            const CK_LDS char *vb = vring + (t % kTSlots) * kTBytes;
-            soft_begin();
-            for (int c = 0; c < 4 * RB; ++c) max_chunk(s_a, c);
-            max_finish();
-            for (int c = 0; c < 4 * RB; ++c) rescale_chunk(c);
-#pragma unroll
-            for (int s16 = 0; s16 < 4; ++s16)
-#pragma unroll
-                for (int rb = 0; rb < RB; ++rb) {
-                    exp_chunk(s_a, s16, rb, 0);
-                    exp_chunk(s_a, s16, rb, 1);
-                }
-            soft_end();
-#pragma unroll
-            for (int s16 = 0; s16 < 4; ++s16)
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    const uint2 lo = lds_read_tr16(vb + vt_off(s16, db, 0));
-                    const uint2 hi = lds_read_tr16(vb + vt_off(s16, db, 1));
-                    const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-#pragma unroll
-                    for (int rb = 0; rb < RB; ++rb)
-                        oacc[rb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pbv[s16][rb], oacc[rb][db], 0, 0, 0);
-                }
-        }
-    }
-
-    // ---- normalise and write whole rows --------------------------------------------
-    // Each wave writes its 32 RB rows through its own slab of the (now idle) rings
-    // (32 rows x 512 B = 16 KB per row block), re-laid out as whole 512-byte rows
-    // so each store instruction writes two contiguous rows.
-    float l_run[RB];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) l_run[rb] = l_part[rb] + __shfl_xor(l_part[rb], 32);
-    __syncthreads();  // every wave is past its last ring read
-    if (!wave_active) return;  // wave-uniform
-    float *base = a.num_splits == 1 ? a.out : a.part_o + (int64_t)sp * a.num_rows * kD;
-    const int my_row = lane & 31;
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-        const float inv = l_run[rb] > 0.f ? 1.0f / l_run[rb] : 0.f;
-        const float lse_v = l_run[rb] > 0.f ? (m_run[rb] + __log2f(l_run[rb])) * kLn2 : -INFINITY;
-        CK_LDS float *slab = (CK_LDS float *)smem + (wid * RB + rb) * (32 * kD);
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int c4 = 0; c4 < 4; ++c4) {
-                const f32x4 o = f32x4{oacc[rb][db][4 * c4 + 0] * inv, oacc[rb][db][4 * c4 + 1] * inv,
-                                      oacc[rb][db][4 * c4 + 2] * inv, oacc[rb][db][4 * c4 + 3] * inv};
-                const int chunk = (8 * db + 2 * c4 + hh) ^ my_row;
-                *reinterpret_cast<CK_LDS f32x4 *>(slab + my_row * kD + chunk * 4) = o;
-            }
-        if (row_valid[rb]) {
-            if (a.num_splits == 1) {
-                const float4 lv = make_float4(lse_v, lse_v, lse_v, lse_v);
-                *reinterpret_cast<float4 *>(a.lse + qrow[rb] * 8 + 4 * hh) = lv;
-            } else if (hh == 0) {
-                a.part_lse[(int64_t)sp * a.num_rows + qrow[rb]] = lse_v;
-            }
-        }
-        // the wave reads back only its own slab: the LDS ops of one wave complete in order
-        const int chunk = lane & 31;
-        const int rbase = wrow0 + rb * 32;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int rr = 2 * j + (lane >> 5);
-            const int64_t qr = __shfl((int)qrow[rb], rr);
-            const f32x4 o = *reinterpret_cast<const CK_LDS f32x4 *>(slab + rr * kD + ((chunk ^ rr) * 4));
-            if (rbase + rr < rows_b) *reinterpret_cast<f32x4 *>(base + qr * kD + chunk * 4) = o;
-        }
-    }
-}
-
 __global__ __launch_bounds__(kWW * 64) void stage1_wide_kernel(Stage1Args a) {
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
     stage1_wide_body<kWW, kWSlots>(a, (CK_LDS char *)smem_raw, blockIdx.x, gridDim.x, threadIdx.x, WgBarrier{});
+}
+
+// 128-row m-tiles: the same whole-row body on 4 waves with a 3-slot ring (the
+// stage-1 role of the fused cascade kernel, as a kernel of its own)
+constexpr int kNLds = wide_lds_bytes<3>();
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void stage1_narrow_kernel(Stage1Args a) {
+    extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+    stage1_wide_body<4, 3>(a, (CK_LDS char *)smem_raw, blockIdx.x, gridDim.x, threadIdx.x, WgBarrier{});
 }
 
 // N-way LSE merge of split partials: 32 threads per row, 4 dims each. One
@@ -727,9 +261,9 @@ int ck::stage1_launch(const void *q, const void *k, const void *v, const int32_t
         hipLaunchKernelGGL(stage1_wide_kernel, dim3((unsigned)grid), dim3(kWW * 64), kWLds, s, a);
     } else {
         static std::atomic<uint64_t> lds_set1{0};
-        rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&stage1_tile_kernel<1>), kTLds, lds_set1);
+        rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&stage1_narrow_kernel), kNLds, lds_set1);
         if (rc != CK_OK) return rc;
-        hipLaunchKernelGGL(stage1_tile_kernel<1>, dim3((unsigned)grid), dim3(kTW * 64), kTLds, s, a);
+        hipLaunchKernelGGL(stage1_narrow_kernel, dim3((unsigned)grid), dim3(256), kNLds, s, a);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
