@@ -65,6 +65,19 @@ def parse():
     return ap.parse_args()
 
 
+def kernel_sources_sha256():
+    """Hash of the HIP kernel sources (csrc/*.hip, *.h): ties a committed traffic profile to
+    the code it was measured on."""
+    import glob
+    import hashlib
+    h = hashlib.sha256()
+    csrc = os.path.join(REPO, "vllm-hust-cascade-kernel_amd", "csrc")
+    for f in sorted(glob.glob(os.path.join(csrc, "*.hip")) + glob.glob(os.path.join(csrc, "*.h"))):
+        h.update(os.path.basename(f).encode())
+        h.update(open(f, "rb").read())
+    return h.hexdigest()
+
+
 def geometric_suffixes(n, seed):
     import numpy as np
     rng = np.random.default_rng(seed)
@@ -265,11 +278,18 @@ def main():
     dom = max(per_op, key=lambda k: per_op[k][0])
     dom_gbs = per_op[dom][1] / (per_op[dom][0] * 1e-3) / 1e9
     # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
-    # (calibrated against a plain copy of known size)
+    # (calibrated against a plain copy of known size); used only while the kernel
+    # sources are the ones that profile was taken from
     traffic = {}
+    traffic_note = "no profile"
     tpath = os.path.join(REPO, "profiles", "pmc_traffic.json")
     if os.path.exists(tpath):
-        traffic = json.load(open(tpath))
+        prof = json.load(open(tpath))
+        if prof.get("sources_sha256") == kernel_sources_sha256():
+            traffic = prof
+            traffic_note = "rocprofv3 FETCH_SIZE/WRITE_SIZE of these kernel sources (profiles/pmc_traffic.md)"
+        else:
+            traffic_note = "profile predates the current kernel sources: traffic not reported"
 
     line = {
         "metric": "cascade-decode attn HBM GB/s (% of peak) + SwiGLU GEMM TFLOP/s at 1 MI355X",
@@ -302,7 +322,8 @@ def main():
         # side by side, most of the step's time) and its epilogue, timed together
         "roofline": {"kernel": "cascade_decode op (" + OP_KERNELS["cascade_decode"] + ")", "bound": "hbm",
                      "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic.get("cascade_decode")},
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic.get("cascade_decode"),
+                     "traffic_source": traffic_note},
         # the slowest op of the reference's three-op composition, for comparison
         "roofline_ops": {"kernel": dom + " op (" + OP_KERNELS[dom] + ")", "bound": "hbm",
                          "achieved": round(dom_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
