@@ -264,6 +264,19 @@ int ck_add_rms_norm_stats(const void *x1, const void *x2, const void *gamma, con
                           void *x_out, float *rstd, void *y, int64_t m_rows, int64_t k_dim,
                           int dtype, int64_t mode, double eps, void *stream);
 
+/* ============================================================================
+ * Health counter of the bounded waits inside the suffix and fused cascade
+ * kernels (ck_suffix_decode, ck_cascade_decode, ck_cascade_decode_noalloc).
+ * Their waves wait on each other only through LDS counters whose waits are
+ * bounded (a hang is never possible); a wait that runs out means a broken
+ * invariant and wrong results, and is counted on the device. *count receives
+ * the number counted on the current device since the library was loaded or
+ * last reset; reset != 0 sets it back to 0. Synchronous: call it after the
+ * kernels of interest have completed (e.g. after hipDeviceSynchronize).
+ * No counterpart in the reference (its waits are hardware pipe flags).
+ * ========================================================================== */
+int ck_wait_giveups(uint64_t *count, int reset);
+
 #ifdef __cplusplus
 }
 #endif

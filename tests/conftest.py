@@ -40,3 +40,16 @@ def pytest_terminal_summary(terminalreporter):
 @pytest.fixture(scope="session")
 def golden_dir():
     return GOLDEN
+
+
+@pytest.fixture
+def no_wait_giveups():
+    """GPU tests of the suffix / fused cascade kernels: none of their bounded
+    waits may run out during the test (ck_wait_giveups stays 0)."""
+    import torch
+    from cascade_amd import abi
+    torch.cuda.synchronize()
+    abi.wait_giveups(reset=True)
+    yield
+    torch.cuda.synchronize()
+    assert abi.wait_giveups() == 0, "a bounded wait in the suffix / cascade kernels ran out"

@@ -101,3 +101,22 @@ def test_capture_needs_decisions_and_prefix_tensors(monkeypatch):
     monkeypatch.setattr(G, "_capturing", lambda: True)
     out, _ = g.decode(q, kv, kv, btp, 1024, bts, sl)     # now capture-safe
     assert out.shape == q.shape
+
+
+def test_prefix_tensor_cache_is_bounded_and_keeps_captured_entries(monkeypatch):
+    """The gate keeps at most PLEN_CACHE prefix-length tensors, evicting the least
+    recently used, but never one a captured graph has read (the graph holds its
+    address); a reused length is served from the cache."""
+    g = G.CascadeGate(32, 8, timer=lambda *a: 1.0)
+    monkeypatch.setattr(G, "_capturing", lambda: False)
+    first = g._prefix_tensor(128, "meta")
+    monkeypatch.setattr(G, "_capturing", lambda: True)
+    assert g._prefix_tensor(128, "meta") is first          # read under capture: pinned
+    monkeypatch.setattr(G, "_capturing", lambda: False)
+    for n in range(1, G.PLEN_CACHE + 50):
+        g._prefix_tensor(128 * (n + 1), "meta")
+        g._prefix_tensor(128 * 2, "meta")                  # kept recent: never evicted
+    assert len(g._plens) == G.PLEN_CACHE
+    assert g._prefix_tensor(128, "meta") is first
+    assert ("meta", 256) in g._plens
+    assert ("meta", 384) not in g._plens                   # the oldest unpinned ones went

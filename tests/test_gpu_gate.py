@@ -11,7 +11,7 @@ from oracle import attention as A
 from oracle.bf16 import bf16_bits, bits_to_f32
 from tests._util import bf16_to_np, torch_bf16
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("no_wait_giveups")]
 DEV = "cuda:0"
 
 

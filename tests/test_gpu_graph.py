@@ -16,7 +16,7 @@ import torch
 from oracle.bf16 import bf16_bits
 from tests._util import torch_bf16
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("no_wait_giveups")]
 DEV = "cuda:0"
 REPLAYS = 3
 

@@ -139,6 +139,25 @@ def test_reference_tieband_gate_one_tile(case, seed):
     assert np.abs(L.astype(np.float64) - L_ref).max() <= 1e-3
 
 
+# Short kv (2-4 tiles of 64 tokens): the kernel's P is rounded on the running max
+# of its own 64-token tiles, the reference's on the 512-column chunk max, so the
+# two grids differ here and the error's tail over ~10^5-10^6 elements depends on
+# the seed. Sixteen seeds of each case must stay within the north-star 2e-3 (and
+# the bf16-P bound against dense attention); each case's margin is printed.
+SHORT_KV = [("min_b1_kv128", 1, [128], 40, 8, 1), ("b64_kv128", 64, [128] * 64, 40, 8, 1),
+            ("flat_T64_kv128", 1, [128], 40, 8, 64),
+            ("varlen_kv65_256", 8, [65, 80, 96, 127, 129, 160, 192, 256], 40, 8, 1)]
+
+
+@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("case", SHORT_KV, ids=[c[0] for c in SHORT_KV])
+def test_short_kv_seed_sweep(case, seed):
+    name, batch, kvs, H, KVH, q_len = case
+    inp = paged_inputs(batch, kvs, H, KVH, seed=100 + seed, q_len=q_len, share_blocks=False, permute=True)
+    out, lse = _run(inp, q_len)
+    _check(inp, out, lse, H, "%s seed%d" % (name, 100 + seed))
+
+
 # More than 128 query rows per kv head with enough kv to fill the chip: the
 # 256-row (8-wave) workgroups, with partial last tiles and varlen requests
 WIDE = [("wide_flat_T64_h64_kv32718", 1, [32718], 64, 8, 64), ("wide_req2_q64_varlen", 2, [30001, 19999], 64, 8, 64)]

@@ -14,7 +14,7 @@ from oracle.inputs import paged_inputs
 from oracle.merge import merge_fp64
 from tests._util import bf16_to_np, torch_bf16
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("no_wait_giveups")]
 DEV = "cuda:0"
 
 

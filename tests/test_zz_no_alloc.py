@@ -12,7 +12,7 @@ import torch
 from oracle.bf16 import bf16_bits
 from tests._util import torch_bf16
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("no_wait_giveups")]
 DEV = "cuda:0"
 
 
@@ -77,6 +77,52 @@ def test_noalloc_matches_workspace_entry_two_calls():
         torch.cuda.synchronize()
         assert torch.equal(out1, out2)
         assert torch.equal(lse1.view(torch.int32), lse2.view(torch.int32))
+
+
+def test_noalloc_under_graph_capture():
+    """The callers it is for capture it: one eager call on the capture stream (the
+    per-device set-up happens there), then the call captured into a HIP graph and
+    replayed twice, each time after fresh q/K/V values and rotated suffix lengths
+    were copied into the captured buffers, with unrelated eager work between the
+    replays. Each replay equals ck_cascade_decode with a caller workspace on the
+    same inputs, bit for bit."""
+    from cascade_amd import abi
+    L = abi.lib()
+    B, H, KVH, P = 24, 32, 8, 2048
+    t = _case(B, H, KVH, P, 3)
+    out = torch.empty(B, H, 128, dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty(B * H, dtype=torch.float32, device=DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        abi.check(L.ck_cascade_decode_noalloc(*_args(t, B, H, KVH, out, lse), side.cuda_stream))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        abi.check(L.ck_cascade_decode_noalloc(*_args(t, B, H, KVH, out, lse),
+                                              torch.cuda.current_stream().cuda_stream))
+    pcap, scap = t["btp"].shape[1] * 128, t["bts"].shape[1] * 128
+    wsb = abi.cascade_plan(B, H, KVH, 128, pcap, scap)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    filler = torch.randn(512, 512, device=DEV)
+    for r in (1, 2):
+        print("noalloc graph replay %d" % r, flush=True)
+        for name in ("q", "k", "v"):
+            t[name].copy_(torch.randn(t[name].shape, generator=gen, device=DEV).to(torch.bfloat16))
+        t["sl"].copy_(torch.roll(t["sl"], r))  # lengths stay within the captured caps
+        g.replay()
+        filler = filler @ filler.t() * 1e-3
+        torch.cuda.synchronize()
+        ref_out = torch.full_like(out, float("nan"))
+        ref_lse = torch.full_like(lse, float("nan"))
+        abi.check(L.ck_cascade_decode(*_args(t, B, H, KVH, ref_out, ref_lse), ws.data_ptr(), wsb,
+                                      torch.cuda.current_stream().cuda_stream), "ck_cascade_decode")
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref_out), "replay %d (O)" % r
+        assert torch.equal(lse.view(torch.int32), ref_lse.view(torch.int32)), "replay %d (LSE)" % r
+    del g
 
 
 def test_noalloc_refuses_shapes_beyond_its_scratch():

@@ -38,6 +38,7 @@ SIGNATURES = {
     "ck_cascade_decode_noalloc": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64,
                                          _i64, _i64, _i64, _i64, _i64, _f32, _i64, _i64, _vp, _vp, _vp]),
     "ck_add_rms_norm_stats": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _int, _i64, _f64, _vp]),
+    "ck_wait_giveups": (_int, [ctypes.POINTER(ctypes.c_uint64), _int]),
 }
 
 CK_DTYPE_BF16 = 0
@@ -93,6 +94,14 @@ def suffix_plan(batch, num_heads, kv_heads, head_dim, kv_cap):
     check(lib().ck_suffix_decode_plan(batch, num_heads, kv_heads, head_dim, kv_cap, ctypes.byref(s),
                                       ctypes.byref(w)), "ck_suffix_decode_plan")
     return s.value, w.value
+
+
+def wait_giveups(reset=False):
+    """Bounded waits of the suffix / fused cascade kernels that ran out on the
+    current device (0 unless an invariant broke); call after a synchronise."""
+    n = ctypes.c_uint64(0)
+    check(lib().ck_wait_giveups(ctypes.byref(n), 1 if reset else 0), "ck_wait_giveups")
+    return n.value
 
 
 def cascade_plan(batch, num_heads, kv_heads, head_dim, prefix_cap, suffix_cap):

@@ -27,12 +27,14 @@ without a decision and for a prefix length it has no device tensor for: measure
 (``choose``) or ``load_json`` the buckets, and make one eager call per prefix
 length (or pass ``prefix_len_tensor``), before capturing.
 """
+import collections
 import json
 import math
 
 import torch
 
 CASCADE = "cascade"
+PLEN_CACHE = 256  # device tensors of prefix lengths kept by a gate (plus any a captured graph read)
 FULL = "full"
 PAGE = 128
 
@@ -100,7 +102,11 @@ class CascadeGate:
         self.timer = timer
         self.margin = margin  # cascade must be faster than full by this factor to be chosen
         self.decisions = {}   # (batch bucket, shared bucket) -> {"choice", "cascade_ms", "full_ms"}
-        self._plens = {}      # (device, prefix length) -> int64 [1] device tensor, made on first use
+        # (device, prefix length) -> int64 [1] device tensor, made on first use; least
+        # recently used first. At most PLEN_CACHE entries, except that an entry a
+        # captured graph has read is never evicted (the graph holds its address).
+        self._plens = collections.OrderedDict()
+        self._plens_captured = set()
 
     # ---- buckets and decisions ---------------------------------------------------
     def bucket(self, batch, shared_len):
@@ -173,7 +179,19 @@ class CascadeGate:
                                    "prefix_len_tensor" % prefix_len)
             t = torch.tensor([int(prefix_len)], dtype=torch.int64, device=device)
             self._plens[k] = t
+            self._evict_prefix_tensors()
+        else:
+            self._plens.move_to_end(k)
+        if _capturing():
+            self._plens_captured.add(k)
         return t
+
+    def _evict_prefix_tensors(self):
+        while len(self._plens) > PLEN_CACHE:
+            old = next((key for key in self._plens if key not in self._plens_captured), None)
+            if old is None:
+                return
+            del self._plens[old]
 
     # ---- persistence ------------------------------------------------------------------
     def to_json(self):

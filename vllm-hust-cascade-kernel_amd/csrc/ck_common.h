@@ -144,10 +144,20 @@ __device__ __forceinline__ float max_xor32(float x) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// A bounded wait that ran out: counted in `counter` (a global word the host
+// reads back) from lane 0 with a vector atomic, so a broken invariant -- a wave
+// that went on past a barrier or into a slot still in use, whose results are
+// then wrong -- never passes silently.
+__device__ __forceinline__ void count_giveup(unsigned int *counter) {
+    if (__lane_id() == 0) __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Workgroup barrier (the stand-alone kernels) and a barrier among the waves of
 // one role of a workgroup that runs two roles side by side: sense-free counting
 // on two LDS words (arrivals, generation). A wave reads the generation before it
-// counts itself in, so the generation cannot move before it has.
+// counts itself in, so the generation cannot move before it has. The wait is
+// bounded (2^24 sleeps, far beyond any real wait); a wait that runs out is
+// counted in *giveups.
 struct WgBarrier {
     __device__ __forceinline__ void sync() const { __syncthreads(); }
 };
@@ -155,6 +165,7 @@ struct GroupBarrier {
     CK_LDS int *cnt;
     CK_LDS int *gen;
     int n;  // waves of the group
+    unsigned int *giveups;
     __device__ __forceinline__ void sync() const {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS writes are done
         const int g0 = __builtin_amdgcn_readfirstlane(*(volatile CK_LDS int *)gen);
@@ -168,8 +179,9 @@ struct GroupBarrier {
                 *(volatile CK_LDS int *)gen = g0 + 1;
             }
         } else {
-            for (int spin = 0; *(volatile CK_LDS int *)gen == g0 && spin < (1 << 24); ++spin)
-                __builtin_amdgcn_s_sleep(1);
+            int spin = 0;
+            for (; *(volatile CK_LDS int *)gen == g0 && spin < (1 << 24); ++spin) __builtin_amdgcn_s_sleep(1);
+            if (spin == (1 << 24)) count_giveup(giveups);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }

@@ -75,6 +75,10 @@
 #include "ck_common.h"
 #include "ck_internal.h"
 
+// Bounded waits of this file's kernels that ran out (a broken invariant, never
+// expected): counted here, read and reset by ck_wait_giveups.
+static __device__ unsigned int g_wait_giveups;
+
 namespace ck {
 namespace {
 
@@ -364,9 +368,11 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             for (int i = tid; i <= a.batch; i += kThr) a.cw_out[i] = cw[i];
         if (scan_flag != nullptr && tid == 0) *(volatile CK_LDS int *)scan_flag = 1;  // after the barrier above
     } else {
-        // the other body's scan (bounded: it always completes, long before this bound)
-        for (int spin = 0; *(volatile CK_LDS int *)scan_flag == 0 && spin < (1 << 22); ++spin)
-            __builtin_amdgcn_s_sleep(1);
+        // the other body's scan (bounded: it always completes, long before this
+        // bound; a wait that runs out is counted)
+        int spin = 0;
+        for (; *(volatile CK_LDS int *)scan_flag == 0 && spin < (1 << 22); ++spin) __builtin_amdgcn_s_sleep(1);
+        if (spin == (1 << 22)) count_giveup(&g_wait_giveups);
     }
 
     const int W = cw[a.batch];
@@ -511,9 +517,14 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         const int r = nclose % R;
         const int want = nclose / R;  // merges the slot has seen before this segment
         // the slot's previous segment must be merged (bounded: a wait that never
-        // ended would mean a broken invariant, and results then are wrong, not hung)
-        for (int spin = 0; *(volatile CK_LDS int *)(xgen + r) != want && spin < (1 << 22); ++spin)
-            __builtin_amdgcn_s_sleep(1);
+        // ended would mean a broken invariant, and results then are wrong, not
+        // hung; such a wait is counted)
+        {
+            int spin = 0;
+            for (; *(volatile CK_LDS int *)(xgen + r) != want && spin < (1 << 22); ++spin)
+                __builtin_amdgcn_s_sleep(1);
+            if (spin == (1 << 22)) count_giveup(&g_wait_giveups);
+        }
         CK_LDS float *xo_r = xo + r * NW * G * kD;
         CK_LDS float *xml_r = xml + r * NW * G * 2;
         if constexpr (TOK && G == 4) {
@@ -1177,7 +1188,7 @@ __global__ __launch_bounds__(512) void cascade_fused_kernel(s1::Stage1Args s1a, 
     __syncthreads();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int role = wave < 4 ? 1 : 0;  // 1: stage-1 waves (suffix chunk 2j + 1 afterwards)
-    const GroupBarrier bar{bars + 2 * (1 - role), bars + 2 * (1 - role) + 1, 4};
+    const GroupBarrier bar{bars + 2 * (1 - role), bars + 2 * (1 - role) + 1, 4, &g_wait_giveups};
     if (role == 1 && (int)blockIdx.x < n1) {
         s1::stage1_wide_body<4, 3>(s1a, smem, blockIdx.x, n1, threadIdx.x, bar);
         bar.sync();  // every stage-1 wave is done with the tile ring
@@ -1411,6 +1422,20 @@ extern "C" int ck_suffix_decode(const void *q, const void *k, const void *v, con
                                  num_blocks, kv_layout, scale, kv_cap, chunks, static_cast<uint16_t *>(out) + b0 * num_heads * kD,
                                  lse + b0 * num_heads, workspace, nullptr, nullptr, nullptr, st, nullptr, 0);
         if (rc != CK_OK) return rc;
+    }
+    return CK_OK;
+}
+
+extern "C" int ck_wait_giveups(uint64_t *count, int reset) {
+    if (!count) return CK_E_NULL_PTR;
+    unsigned int v = 0;
+    hipError_t e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_wait_giveups), sizeof(v), 0, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return static_cast<int>(e);
+    *count = v;
+    if (reset) {
+        const unsigned int zero = 0;
+        e = hipMemcpyToSymbol(HIP_SYMBOL(g_wait_giveups), &zero, sizeof(zero), 0, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return static_cast<int>(e);
     }
     return CK_OK;
 }

@@ -146,7 +146,7 @@ std::tuple<at::Tensor, at::Tensor> fa_fp32_stage1_impl(const at::Tensor &query, 
     const int64_t block_size = key.size(1);
     const int64_t batch = actual_q_seqlens.numel();
     TORCH_CHECK(actual_kv_seqlens.numel() == batch, "fa_fp32_stage1: seqlen tensors must have batch entries");
-    TORCH_CHECK(embed == 128, "fa_fp32_stage1: only head dim 128 is supported (L1TileShape::K constraint)");
+    TORCH_CHECK(embed == 128, "fa_fp32_stage1: only head dim 128 is supported (the kernels' MFMA tiles span 128 dims)");
     TORCH_CHECK(block_size == 128, "fa_fp32_stage1: only paged blockSize 128 is supported");
     TORCH_CHECK(kv_heads > 0 && num_heads % kv_heads == 0, "fa_fp32_stage1: numHeads must be a multiple of kvHeads");
     TORCH_CHECK(key.size(3) == embed, "fa_fp32_stage1: key/value head dim must equal the query head dim");
