@@ -277,6 +277,28 @@ int ck_add_rms_norm_stats(const void *x1, const void *x2, const void *gamma, con
  * ========================================================================== */
 int ck_wait_giveups(uint64_t *count, int reset);
 
+/* ============================================================================
+ * Benchmark-only probes of the measured ceilings the roofline fractions are
+ * quoted against (no production path calls them). They take the measurement
+ * role of the reference's benchmark-only bandwidth probe
+ * (OPS/bw_probe/design.md:1-30); the code and access patterns are this
+ * library's own.
+ *   ck_bw_probe  variant 0: stream-read `bytes` from src (each lane folds its
+ *                16-byte loads into one word of `sink`, sink_bytes >=
+ *                CK_PROBE_SINK_BYTES); variant 1: copy `bytes` from src to dst.
+ *                bytes % 16 == 0; src, dst 16-byte aligned.
+ *   ck_mfma_probe  iterations (1 .. 2^24) rounds of 16 independent
+ *                v_mfma_f32_32x32x16_bf16 per wave on register operands, two
+ *                waves per SIMD; *flops receives the work launched (set before
+ *                the kernel runs; time it with events on `stream`); sink as above.
+ * ========================================================================== */
+#define CK_PROBE_SINK_BYTES (2ll << 20)
+
+int ck_bw_probe(const void *src, void *dst, int64_t bytes, int variant, void *sink, int64_t sink_bytes,
+                void *stream);
+
+int ck_mfma_probe(int64_t iterations, void *sink, int64_t sink_bytes, double *flops, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,19 @@ def test_library_exports_every_header_symbol():
         assert hasattr(handle, n), n
 
 
+def test_probe_argument_validation_without_launch():
+    L = abi.lib()
+    p = ctypes.c_void_p(256)  # never dereferenced: every call below fails validation first
+    assert L.ck_bw_probe(p, None, 8, 0, p, abi.PROBE_SINK_BYTES, None) == -1           # bytes < 16
+    assert L.ck_bw_probe(p, None, 24, 0, p, abi.PROBE_SINK_BYTES, None) == -1          # bytes % 16
+    assert L.ck_bw_probe(p, None, 1024, 2, p, abi.PROBE_SINK_BYTES, None) == -1        # variant
+    assert L.ck_bw_probe(p, None, 1024, 1, None, 0, None) == -2                        # copy needs dst
+    assert L.ck_bw_probe(p, None, 1024, 0, p, abi.PROBE_SINK_BYTES - 4, None) == -3    # short sink
+    f = ctypes.c_double(0)
+    assert L.ck_mfma_probe(0, p, abi.PROBE_SINK_BYTES, ctypes.byref(f), None) == -1
+    assert L.ck_mfma_probe(16, p, 1024, ctypes.byref(f), None) == -3
+
+
 def test_error_strings():
     assert abi.error_string(0) == "success"
     for code in (-1, -2, -3, -4):

@@ -171,6 +171,32 @@ def test_wide_row_tiles(case):
     _check(inp, out, lse, H, name)
 
 
+# The 256-row kernel on short and ragged splits: a ring that never fills (one to a
+# few tiles per split), partial last tiles, a 1-token split, and rows that leave the
+# last waves of the m-tile idle (200 rows per kv head). batch x kv heads reaches 256
+# workgroups, so the plan picks the 256-row tile.
+def _ragged(n, lo, hi, seed):
+    rng = np.random.default_rng(seed)
+    kvs = rng.integers(lo, hi + 1, size=n)
+    kvs[0], kvs[-1] = 1, 64
+    return [int(x) for x in kvs]
+
+
+WIDE_RAGGED = [("wide_b32_q64_kv1_300", 32, _ragged(32, 1, 300, 1), 32, 8, 64),
+               ("wide_b40_q50_kv1_1100", 40, _ragged(40, 1, 1100, 2), 32, 8, 50)]
+
+
+@pytest.mark.parametrize("case", WIDE_RAGGED, ids=[c[0] for c in WIDE_RAGGED])
+def test_wide_short_ragged_splits(case):
+    name, batch, kvs, H, KVH, q_len = case
+    inp = paged_inputs(batch, kvs, H, KVH, seed=13, q_len=q_len, share_blocks=False, permute=True)
+    out, lse = _run(inp, q_len)
+    _check(inp, out, lse, H, name)
+    out2, lse2 = _run(inp, q_len)  # run to run bit-identical
+    assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
+    assert np.array_equal(lse.view(np.uint32), lse2.view(np.uint32))
+
+
 # test_lse_flatten_regression.py:30-47: B=1 flattened form, q_len = T
 FLAT = [("flat_T64_kv128", 64, 40, 8, 128), ("flat_T64_kv4356", 64, 40, 8, 4356),
         ("flat_T8_3b", 8, 16, 2, 4096), ("flat_T17_bnd", 17, 40, 8, 4096), ("flat_T63_odd", 63, 40, 8, 4096)]

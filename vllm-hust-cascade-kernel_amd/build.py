@@ -26,7 +26,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
 KERNEL_SOURCES = ["abi.hip", "lse_merge.hip", "fa_stage1.hip", "suffix_decode.hip", "cascade.hip",
-                  "gateup_swiglu.hip", "add_rms_norm.hip"]
+                  "gateup_swiglu.hip", "add_rms_norm.hip", "probe.hip"]
 
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fno-gpu-rdc",

@@ -39,7 +39,10 @@ SIGNATURES = {
                                          _i64, _i64, _i64, _i64, _i64, _f32, _i64, _i64, _vp, _vp, _vp]),
     "ck_add_rms_norm_stats": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _int, _i64, _f64, _vp]),
     "ck_wait_giveups": (_int, [ctypes.POINTER(ctypes.c_uint64), _int]),
+    "ck_bw_probe": (_int, [_vp, _vp, _i64, _int, _vp, _i64, _vp]),
+    "ck_mfma_probe": (_int, [_i64, _vp, _i64, ctypes.POINTER(ctypes.c_double), _vp]),
 }
+PROBE_SINK_BYTES = 2 << 20
 
 CK_DTYPE_BF16 = 0
 CK_DTYPE_F32 = 1
