@@ -317,7 +317,7 @@ __device__ __forceinline__ void stage1_wide_body(const Stage1Args &a, CK_LDS cha
             const float4 lv = make_float4(lse_v, lse_v, lse_v, lse_v);
             *reinterpret_cast<float4 *>(a.lse + qrow * 8 + 4 * hh) = lv;
         } else if (hh == 0) {
-            a.part_lse[(int64_t)sp * a.num_rows + qrow] = lse_v;
+            __builtin_nontemporal_store(lse_v, a.part_lse + (int64_t)sp * a.num_rows + qrow);
         }
     }
     float *base = a.num_splits == 1 ? a.out : a.part_o + (int64_t)sp * a.num_rows * kD;
@@ -327,7 +327,8 @@ __device__ __forceinline__ void stage1_wide_body(const Stage1Args &a, CK_LDS cha
         const int rr = 2 * j + (lane >> 5);
         const int64_t qr = __shfl((int)qrow, rr);
         const f32x4 o = *reinterpret_cast<const CK_LDS f32x4 *>(slab + rr * kD + ((chunk ^ rr) * 4));
-        if (wrow0 + rr < rows_b) *reinterpret_cast<f32x4 *>(base + qr * kD + chunk * 4) = o;
+        // non-temporal: read once, by another kernel (combine, cascade epilogue)
+        if (wrow0 + rr < rows_b) __builtin_nontemporal_store(o, reinterpret_cast<f32x4 *>(base + qr * kD + chunk * 4));
     }
 }
 

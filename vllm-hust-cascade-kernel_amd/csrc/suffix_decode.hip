@@ -335,12 +335,17 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     // ---- lengths and window prefix sums (kPer sequences per thread, block scan) ----
     if (scan_src == nullptr) {
         constexpr int kPer = kMaxBatch / kThr;
+        // every load goes out before any is used (one round trip, not kPer): the
+        // index is clamped into the batch, and entries past it are dropped below
+        int64_t raw[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) raw[j] = a.kv_seqlens[min(kPer * tid + j, a.batch - 1)];
         int lv[kPer];
         int local = 0;
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
             const int i = kPer * tid + j;
-            const int ln = i < a.batch ? (int)clamp_len(a, a.kv_seqlens[i]) : 0;
+            const int ln = i < a.batch ? (int)clamp_len(a, raw[j]) : 0;
             if (i < a.batch) len[i] = ln;
             lv[j] = (ln + kWin - 1) / kWin;
             local += lv[j];
@@ -602,8 +607,9 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                     } else {
                         const int64_t pidx =
                             (((int64_t)g * a.chunks + chunk) * 2 + (head_part ? 0 : 1)) * G + h;
-                        *reinterpret_cast<float4 *>(a.part_o + pidx * kD + 4 * d4) =
-                            make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+                        // non-temporal: read once, by the fix-up or cascade epilogue kernel
+                        __builtin_nontemporal_store(f32x4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv},
+                                                    reinterpret_cast<f32x4 *>(a.part_o + pidx * kD + 4 * d4));
                         if (d4 == 0) a.part_lse[pidx] = lse_v;
                     }
                 }
