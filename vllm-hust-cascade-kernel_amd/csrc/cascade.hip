@@ -14,8 +14,11 @@
 //   3. the cascade epilogue: per (sequence, kv head) it folds the stage-1
 //      partials and the suffix partials and merges the two results into the
 //      final bf16 O and the merged LSE.
-// Three launches instead of five (stage-1, combine, suffix, fix-up, merge),
-// and neither partial result makes an extra round trip through HBM.
+// When the batch fits one launch group and stage-1 is small enough to hide
+// beside the suffix stream, 1 and 2 are one fused kernel (suffix_decode.hip):
+// two launches in all; otherwise three. Either way fewer than the five of the
+// composed ops (stage-1, combine, suffix, fix-up, merge), and neither partial
+// result makes an extra round trip through HBM.
 //
 // ck_cascade_decode_noalloc is the same call for callers that cannot allocate
 // (code under HIP-graph capture, serving loops that forbid allocation): its
