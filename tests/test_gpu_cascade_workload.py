@@ -121,9 +121,11 @@ def run_cascade(q, k, v, bt_pre, P, bt_suf, suf):
 
 def check_rows(name, got, lse, O_ref, L_ref, what):
     err = np.abs(got - O_ref)
-    bound = 2e-3 + 2.0 ** -8 * np.abs(O_ref)
+    half_ulp = 2.0 ** -8 * np.abs(O_ref)  # the bf16 output's own rounding
+    bound = 2e-3 + half_ulp
     rel = np.abs(lse - L_ref) / np.maximum(np.abs(L_ref), 1.0)
-    record_margin("%s vs %s" % (name, what), err.max(), 2e-3, rel.max(), 1e-4)
+    # recorded: the largest error beyond the output rounding, against the 2e-3 tolerance
+    record_margin("%s vs %s" % (name, what), np.maximum(err - half_ulp, 0.0).max(), 2e-3, rel.max(), 1e-4)
     assert np.all(err <= bound), (what, err.max(), np.unravel_index(np.argmax(err - bound), err.shape))
     assert rel.max() <= 1e-4, (what, rel.max())
 
