@@ -56,7 +56,10 @@
 //   LDS atomic; the last of the 8 waves merges the 8 partials and writes the
 //   result while the others go on. A wave waits for a ring slot only if it runs
 //   a whole ring ahead of the slowest wave, which itself never waits, so every
-//   wait ends.
+//   wait ends. (The fused kernel's token-major body splits each merge over its
+//   4 waves instead, once all partials are in: one wave doing the whole merge
+//   fell behind the others by it at every close, and the workgroup waits for
+//   its slowest wave.)
 // * Cascade (stage 1 + suffix + merge): one fused kernel, one workgroup per CU.
 //   Waves 0-3 run the stage-1 body (MFMA, LDS tiles: matrix cores and LDS),
 //   waves 4-7 stream suffix windows (memory pipe and vector ALU); each role
@@ -120,8 +123,10 @@ constexpr int kFusedTokDepth = 2;  // token-major: 16 registers per window and l
 constexpr int kFusedSplit = 192;
 static_assert(kFusedSplit >= 128 && kFusedSplit < 256, "ChunkMap::none_empty assumes a share in [1/2, 1)");
 
-// LDS layout (bytes) of the stream body for G query heads per group and NW waves
-template <int G, int NW>
+// LDS layout (bytes) of the stream body for G query heads per group and NW waves;
+// STASH (the token-major body) adds the merged results of a phase's segments,
+// held until the phase's window loop is done.
+template <int G, int NW, bool STASH = false>
 struct SfxLds {
     static constexpr int kCw = 0;                                        // int cw[kMaxBatch + 1]
     static constexpr int kLen = ((kMaxBatch + 1) * 4 + 15) / 16 * 16;   // int len[kMaxBatch]
@@ -132,10 +137,14 @@ struct SfxLds {
     static constexpr int kX = G <= 4 ? 2 : 1;                            // exchange ring slots
     static constexpr int kXo = kQs + kQSlots * G * kD * 2;               // float xo[kX][NW][G][kD]
     static constexpr int kXml = kXo + kX * NW * G * kD * 4;              // float xml[kX][NW][G][2]
-    static constexpr int kXsync = kXml + kX * NW * G * 2 * 4;            // int cnt[kX], gen[kX]
-    static constexpr int kBar = kXsync + 2 * kX * 4;                     // int bar[2] (group barrier)
-    static constexpr int kBytes = (kBar + 8 + 15) / 16 * 16;
-    static_assert(kTab % 16 == 0 && kPw % 16 == 0 && kQs % 16 == 0 && kXo % 16 == 0 && kXml % 8 == 0,
+    static constexpr int kXsync = kXml + kX * NW * G * 2 * 4;            // int cnt[kX], gen[kX], done[kX]
+    static constexpr int kBar = kXsync + 3 * kX * 4;                     // int bar[2] (group barrier)
+    static constexpr int kSo = (kBar + 8 + 15) / 16 * 16;                // float so[kQSlots][G][kD] (STASH)
+    static constexpr int kSl = kSo + (STASH ? kQSlots * G * kD * 4 : 0); // float sl[kQSlots][G]
+    static constexpr int kSb = kSl + (STASH ? kQSlots * G * 4 : 0);      // int sb[kQSlots]
+    static constexpr int kBytes = (kSb + (STASH ? kQSlots * 4 : 0) + 15) / 16 * 16;
+    static_assert(kTab % 16 == 0 && kPw % 16 == 0 && kQs % 16 == 0 && kXo % 16 == 0 && kXml % 8 == 0 &&
+                      kSo % 16 == 0,
                   "aligned LDS rows");
 };
 static_assert(SfxLds<kMaxGroup, kWaves>::kBytes <= 80 * 1024, "two stand-alone workgroups per CU");
@@ -290,6 +299,11 @@ __device__ __forceinline__ int64_t clamp_len(const SuffixArgs &a, int64_t kvl) {
 //   makes no LDS access besides one table read, and its arithmetic never waits
 //   on the LDS pipe (which the fused kernel's stage-1 waves keep busy). 16
 //   accumulators per head, summed over the 8 token slots when a segment closes.
+//   The merged result of a segment waits in an LDS stash, and the role's waves
+//   write a phase's results out together after its window loop: a store in the
+//   loop would count in the same vmcnt as the window loads, so every later wait
+//   of the merging wave would also wait for its acknowledgement (or for loads
+//   issued after it), a stall of about a round trip per merge.
 //
 // Two bodies on one CU may share one scan: the body given scan_src (the other
 // body's LDS) skips its own, waits until scan_flag is set and reads the other's
@@ -305,7 +319,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     constexpr int kThr = NW * 64;
     constexpr int kWin = 8 * NW;         // tokens per window
     constexpr int kWpp = kPage / kWin;   // windows per page
-    using L = SfxLds<G, NW>;
+    using L = SfxLds<G, NW, TOK>;
     CK_LDS int *cw = (CK_LDS int *)((scan_src ? scan_src : smem) + L::kCw);
     CK_LDS int *len = (CK_LDS int *)((scan_src ? scan_src : smem) + L::kLen);
     CK_LDS int *wtot = (CK_LDS int *)(smem + L::kWtot);
@@ -316,6 +330,10 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     CK_LDS float *xml = (CK_LDS float *)(smem + L::kXml);
     CK_LDS int *xcnt = (CK_LDS int *)(smem + L::kXsync);  // waves counted into each slot
     CK_LDS int *xgen = xcnt + R;                             // merges completed in each slot
+    CK_LDS int *xdone = xgen + R;                            // TOK: waves done merging each slot
+    CK_LDS float *so = (CK_LDS float *)(smem + L::kSo);      // TOK: merged O of the phase's segments
+    CK_LDS float *sl = (CK_LDS float *)(smem + L::kSl);      // TOK: their LSE
+    CK_LDS int *sb = (CK_LDS int *)(smem + L::kSb);          // TOK: their sequence
 
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
@@ -330,6 +348,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     if (tid < R) {
         xcnt[tid] = 0;
         xgen[tid] = 0;
+        xdone[tid] = 0;
     }
 
     // ---- lengths and window prefix sums (kPer sequences per thread, block scan) ----
@@ -481,9 +500,91 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         x1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(w.o + 128), 0, 0));
     };
 
+    // The merged result of sequence b's segment for query head h, dims 4 d4 .. 4 d4
+    // + 3 (O normalised): bf16 O and the LSE when the segment is the whole
+    // sequence, else an fp32 partial in the chunk's head or tail slot.
+    auto write_result = [&](int b, int h, int d4, f32x4 on, float lse_v) __attribute__((always_inline)) {
+        const bool head_part = cw[b] < w0;
+        const bool tail_part = cw[b + 1] > w1;
+        if (!head_part && !tail_part) {
+            const int64_t row = (int64_t)b * a.num_heads + g * G + h;
+            *reinterpret_cast<uint2 *>(a.out + row * kD + 4 * d4) =
+                make_uint2(pack_bf16x2(on[0], on[1]), pack_bf16x2(on[2], on[3]));
+            if (d4 == 0) a.lse[row] = lse_v;
+        } else {
+            const int64_t pidx = (((int64_t)g * a.chunks + chunk) * 2 + (head_part ? 0 : 1)) * G + h;
+            // non-temporal: read once, by the fix-up or cascade epilogue kernel
+            __builtin_nontemporal_store(on, reinterpret_cast<f32x4 *>(a.part_o + pidx * kD + 4 * d4));
+            if (d4 == 0) a.part_lse[pidx] = lse_v;
+        }
+    };
+
+    // Merges query-head / dim pair u (h = u / 32, dims 4 (u % 32) .. + 3) of the NW
+    // partials in exchange slot r: TOK into stash entry e, else straight out for
+    // sequence b.
+    auto merge_pair = [&](int u, int r, int b, int e) __attribute__((always_inline)) {
+        const CK_LDS float *xo_r = xo + r * NW * G * kD;
+        const CK_LDS float *xml_r = xml + r * NW * G * 2;
+        const int h = u >> 5, d4 = u & 31;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) mx = fmaxf(mx, xml_r[(ww * G + h) * 2]);
+        const float mz = mx == -INFINITY ? 0.f : mx;
+        float lt = 0.f;
+        f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) {
+            const float f = exp2_fast(xml_r[(ww * G + h) * 2] - mz);
+            lt = fmaf(xml_r[(ww * G + h) * 2 + 1], f, lt);
+            const f32x4 xa = *reinterpret_cast<const CK_LDS f32x4 *>(xo_r + (ww * G + h) * kD + 4 * d4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = fmaf(xa[i], f, o[i]);
+        }
+        const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+        const float lse_v = lt > 0.f ? (mx + __log2f(lt)) * kLn2 : -INFINITY;
+        const f32x4 on = f32x4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
+        if constexpr (TOK) {
+            *reinterpret_cast<CK_LDS f32x4 *>(so + (e * G + h) * kD + 4 * d4) = on;
+            if (d4 == 0) sl[e * G + h] = lse_v;
+        } else {
+            write_result(b, h, d4, on, lse_v);
+        }
+    };
+
+    // TOK: this wave's share of the merge of close k (exchange slot k % R, sequence
+    // b, stash entry e) once all NW partials are in (bounded wait: every wave
+    // closes the same segments), so no single wave carries the whole merge; the
+    // last wave done frees the slot.
+    auto merge_share = [&](int k, int b, int e) __attribute__((always_inline)) {
+        const int r = k % R;
+        {
+            int spin = 0;
+            for (; *(volatile CK_LDS int *)(xcnt + r) < NW && spin < (1 << 22); ++spin) __builtin_amdgcn_s_sleep(1);
+            if (spin == (1 << 22)) count_giveup(&g_wait_giveups);
+        }
+        asm volatile("" ::: "memory");
+        constexpr int kPer = 32 * G / NW;  // pairs per wave
+        static_assert(!TOK || (kPer * NW == 32 * G && kPer <= 64), "pairs split evenly over the waves");
+        if (lane < kPer) merge_pair(wid * kPer + lane, r, b, e);
+        if (wid == 0 && lane == 0) sb[e] = b;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        int done = 0;
+        if (lane == 0) done = __hip_atomic_fetch_add(xdone + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        done = __builtin_amdgcn_readfirstlane(done);
+        if (done == NW - 1) {
+            // every wave is past its wait and its reads: free the slot, then publish
+            if (lane == 0) {
+                xcnt[r] = 0;
+                xdone[r] = 0;
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lane == 0) xgen[r] = k / R + 1;
+        }
+    };
+
     // Closes segment b (sequence b's windows in this range): folds the lanes' partial
     // sums, hands the wave's (O, m, l) to the exchange ring, and the last wave in
-    // merges the NW partials and writes the result.
+    // merges the NW partials and writes the result (TOK: into the phase's stash).
     auto close_seg = [&](int b) __attribute__((always_inline)) {
         // token-major with 4 heads: a reduce-scatter over the 8 token slots. The
         // 64 accumulators of a lane, flat index f = 16 h + e, are halved twice by
@@ -569,56 +670,26 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         }
         // a wave's LDS operations complete in order: its rows are in before it counts itself
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        int old = 0;
-        if (lane == 0) old = __hip_atomic_fetch_add(xcnt + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        old = __builtin_amdgcn_readfirstlane(old);
-        if (old == NW - 1) {
-            // the last wave in: merge the 8 partials of every query head
-            asm volatile("" ::: "memory");
+        if constexpr (TOK) {
+            if (lane == 0) __hip_atomic_fetch_add(xcnt + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            merge_share(nclose, b, qslot);
+        } else {
+            int old = 0;
+            if (lane == 0) old = __hip_atomic_fetch_add(xcnt + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            old = __builtin_amdgcn_readfirstlane(old);
+            if (old == NW - 1) {
+                // the last wave in: merge the NW partials of every query head
+                asm volatile("" ::: "memory");
 #pragma unroll 1
-            for (int u0 = 0; u0 < 32 * G; u0 += 64) {
-                const int u = u0 + lane;
-                if (u < 32 * G) {
-                    const int h = u >> 5, d4 = u & 31;
-                    float mx = -INFINITY;
-#pragma unroll
-                    for (int ww = 0; ww < NW; ++ww) mx = fmaxf(mx, xml_r[(ww * G + h) * 2]);
-                    const float mz = mx == -INFINITY ? 0.f : mx;
-                    float lt = 0.f;
-                    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int ww = 0; ww < NW; ++ww) {
-                        const float f = exp2_fast(xml_r[(ww * G + h) * 2] - mz);
-                        lt = fmaf(xml_r[(ww * G + h) * 2 + 1], f, lt);
-                        const f32x4 xa =
-                            *reinterpret_cast<const CK_LDS f32x4 *>(xo_r + (ww * G + h) * kD + 4 * d4);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) o[e] = fmaf(xa[e], f, o[e]);
-                    }
-                    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-                    const float lse_v = lt > 0.f ? (mx + __log2f(lt)) * kLn2 : -INFINITY;
-                    const bool head_part = cw[b] < w0;
-                    const bool tail_part = cw[b + 1] > w1;
-                    if (!head_part && !tail_part) {
-                        const int64_t row = (int64_t)b * a.num_heads + g * G + h;
-                        *reinterpret_cast<uint2 *>(a.out + row * kD + 4 * d4) = make_uint2(
-                            pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv));
-                        if (d4 == 0) a.lse[row] = lse_v;
-                    } else {
-                        const int64_t pidx =
-                            (((int64_t)g * a.chunks + chunk) * 2 + (head_part ? 0 : 1)) * G + h;
-                        // non-temporal: read once, by the fix-up or cascade epilogue kernel
-                        __builtin_nontemporal_store(f32x4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv},
-                                                    reinterpret_cast<f32x4 *>(a.part_o + pidx * kD + 4 * d4));
-                        if (d4 == 0) a.part_lse[pidx] = lse_v;
-                    }
+                for (int u0 = 0; u0 < 32 * G; u0 += 64) {
+                    if (u0 + lane < 32 * G) merge_pair(u0 + lane, r, b, 0);
                 }
+                // free the slot: reset its count, then publish the merge
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                if (lane == 0) xcnt[r] = 0;
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                if (lane == 0) xgen[r] = want + 1;
             }
-            // free the slot: reset its count, then publish the merge
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (lane == 0) xcnt[r] = 0;
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (lane == 0) xgen[r] = want + 1;
         }
         ++nclose;
         ++qslot;
@@ -927,6 +998,18 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             }
         });
         drain_tok(np);
+        if constexpr (TOK) {
+            // the phase's merged results out, by every wave of the role: each merge
+            // is done once every wave is past its last close
+            bar.sync();
+            const int nseg = qslot;  // segments closed in this phase (the same in every wave)
+            for (int i = tid; i < nseg * G * 32; i += kThr) {
+                const int e = i / (G * 32), u = i % (G * 32);
+                const int h = u >> 5, d4 = u & 31;
+                write_result(sb[e], h, d4, *reinterpret_cast<const CK_LDS f32x4 *>(so + (e * G + h) * kD + 4 * d4),
+                             sl[e * G + h]);
+            }
+        }
         p0 = p1;
     }
 }
@@ -1181,15 +1264,19 @@ __global__ __launch_bounds__(kMaxGroup * 32) void cascade_epilogue_kernel(Epilog
 // for the other.
 constexpr int kFusedS1Lds = s1::wide_lds_bytes<3>();
 template <int G>
-constexpr int fused_lds_bytes() { return kFusedS1Lds + SfxLds<G, 4>::kBytes + 32; }
-static_assert(fused_lds_bytes<kMaxGroup>() <= 160 * 1024, "one fused workgroup per CU");
-static_assert(SfxLds<kMaxGroup, 4>::kBytes <= kFusedS1Lds, "the stage-1 waves' stream body fits the tile ring");
+using FusedSfx = SfxLds<G, 4, (G <= 4)>;  // the stream body's layout on 4 waves (token-major up to 4 heads)
+template <int G>
+constexpr int fused_lds_bytes() { return kFusedS1Lds + FusedSfx<G>::kBytes + 32; }
+static_assert(fused_lds_bytes<4>() <= 160 * 1024 && fused_lds_bytes<kMaxGroup>() <= 160 * 1024,
+              "one fused workgroup per CU");
+static_assert(FusedSfx<4>::kBytes <= kFusedS1Lds && FusedSfx<kMaxGroup>::kBytes <= kFusedS1Lds,
+              "the stage-1 waves' stream body fits the tile ring");
 
 template <int G>
 __global__ __launch_bounds__(512) void cascade_fused_kernel(s1::Stage1Args s1a, int n1, SuffixArgs sa, int n2) {
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
     CK_LDS char *smem = (CK_LDS char *)smem_raw;
-    CK_LDS int *bars = (CK_LDS int *)(smem + kFusedS1Lds + SfxLds<G, 4>::kBytes);
+    CK_LDS int *bars = (CK_LDS int *)(smem + kFusedS1Lds + FusedSfx<G>::kBytes);
     if (threadIdx.x < 5) bars[threadIdx.x] = 0;  // two role barriers, the scan flag
     __syncthreads();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
