@@ -137,8 +137,8 @@ struct SfxLds {
     static constexpr int kX = G <= 4 ? 2 : 1;                            // exchange ring slots
     static constexpr int kXo = kQs + kQSlots * G * kD * 2;               // float xo[kX][NW][G][kD]
     static constexpr int kXml = kXo + kX * NW * G * kD * 4;              // float xml[kX][NW][G][2]
-    static constexpr int kXsync = kXml + kX * NW * G * 2 * 4;            // int cnt[kX], gen[kX], done[kX]
-    static constexpr int kBar = kXsync + 3 * kX * 4;                     // int bar[2] (group barrier)
+    static constexpr int kXsync = kXml + kX * NW * G * 2 * 4;            // int cnt[kX], gen[kX]
+    static constexpr int kBar = kXsync + 2 * kX * 4;                     // int bar[2] (group barrier)
     static constexpr int kSo = (kBar + 8 + 15) / 16 * 16;                // float so[kQSlots][G][kD] (STASH)
     static constexpr int kSl = kSo + (STASH ? kQSlots * G * kD * 4 : 0); // float sl[kQSlots][G]
     static constexpr int kSb = kSl + (STASH ? kQSlots * G * 4 : 0);      // int sb[kQSlots]
@@ -330,7 +330,6 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     CK_LDS float *xml = (CK_LDS float *)(smem + L::kXml);
     CK_LDS int *xcnt = (CK_LDS int *)(smem + L::kXsync);  // waves counted into each slot
     CK_LDS int *xgen = xcnt + R;                             // merges completed in each slot
-    CK_LDS int *xdone = xgen + R;                            // TOK: waves done merging each slot
     CK_LDS float *so = (CK_LDS float *)(smem + L::kSo);      // TOK: merged O of the phase's segments
     CK_LDS float *sl = (CK_LDS float *)(smem + L::kSl);      // TOK: their LSE
     CK_LDS int *sb = (CK_LDS int *)(smem + L::kSb);          // TOK: their sequence
@@ -348,7 +347,6 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     if (tid < R) {
         xcnt[tid] = 0;
         xgen[tid] = 0;
-        xdone[tid] = 0;
     }
 
     // ---- lengths and window prefix sums (kPer sequences per thread, block scan) ----
@@ -553,13 +551,20 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
 
     // TOK: this wave's share of the merge of close k (exchange slot k % R, sequence
     // b, stash entry e) once all NW partials are in (bounded wait: every wave
-    // closes the same segments), so no single wave carries the whole merge; the
-    // last wave done frees the slot.
+    // closes the same segments), so no single wave carries the whole merge. The
+    // slot's arrival count only grows, NW per use, so use k / R is complete at
+    // NW (k / R + 1) and nothing is reset or published: a wave at close k has
+    // passed close k - 1's wait, for which every wave arrived after its reads of
+    // close k - 2, the slot's previous use. Each step of a close costs an LDS round
+    // trip, slow while the stage-1 waves keep the LDS busy, so the close has few.
     auto merge_share = [&](int k, int b, int e) __attribute__((always_inline)) {
+        static_assert(!TOK || R == 2, "the slot reuse argument above takes two slots");
         const int r = k % R;
+        const int target = NW * (k / R + 1);
         {
             int spin = 0;
-            for (; *(volatile CK_LDS int *)(xcnt + r) < NW && spin < (1 << 22); ++spin) __builtin_amdgcn_s_sleep(1);
+            for (; *(volatile CK_LDS int *)(xcnt + r) < target && spin < (1 << 22); ++spin)
+                __builtin_amdgcn_s_sleep(1);
             if (spin == (1 << 22)) count_giveup(&g_wait_giveups);
         }
         asm volatile("" ::: "memory");
@@ -567,19 +572,6 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         static_assert(!TOK || (kPer * NW == 32 * G && kPer <= 64), "pairs split evenly over the waves");
         if (lane < kPer) merge_pair(wid * kPer + lane, r, b, e);
         if (wid == 0 && lane == 0) sb[e] = b;
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        int done = 0;
-        if (lane == 0) done = __hip_atomic_fetch_add(xdone + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        done = __builtin_amdgcn_readfirstlane(done);
-        if (done == NW - 1) {
-            // every wave is past its wait and its reads: free the slot, then publish
-            if (lane == 0) {
-                xcnt[r] = 0;
-                xdone[r] = 0;
-            }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (lane == 0) xgen[r] = k / R + 1;
-        }
     };
 
     // Closes segment b (sequence b's windows in this range): folds the lanes' partial
@@ -622,10 +614,10 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         }
         const int r = nclose % R;
         const int want = nclose / R;  // merges the slot has seen before this segment
-        // the slot's previous segment must be merged (bounded: a wait that never
-        // ended would mean a broken invariant, and results then are wrong, not
-        // hung; such a wait is counted)
-        {
+        // dims-major: the slot's previous segment must be merged (bounded: a wait
+        // that never ended would mean a broken invariant, and results then are
+        // wrong, not hung; such a wait is counted). Token-major: see merge_share.
+        if constexpr (!TOK) {
             int spin = 0;
             for (; *(volatile CK_LDS int *)(xgen + r) != want && spin < (1 << 22); ++spin)
                 __builtin_amdgcn_s_sleep(1);
@@ -668,8 +660,11 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                 xml_r[(wid * G + h) * 2 + 1] = l[h];
             }
         }
-        // a wave's LDS operations complete in order: its rows are in before it counts itself
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // a wave's LDS operations are performed in the order it issues them: its rows
+        // are in before its arrival counts (token-major: no wait for that; the
+        // dims-major path waits, as before)
+        if constexpr (TOK) asm volatile("" ::: "memory");
+        else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if constexpr (TOK) {
             if (lane == 0) __hip_atomic_fetch_add(xcnt + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             merge_share(nclose, b, qslot);
