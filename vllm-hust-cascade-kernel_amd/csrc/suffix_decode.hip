@@ -1279,6 +1279,12 @@ __global__ __launch_bounds__(512) void cascade_fused_kernel(s1::Stage1Args s1a, 
     const GroupBarrier bar{bars + 2 * (1 - role), bars + 2 * (1 - role) + 1, 4, &g_wait_giveups};
     if (role == 1 && (int)blockIdx.x < n1) {
         s1::stage1_wide_body<4, 3>(s1a, smem, blockIdx.x, n1, threadIdx.x, bar);
+        // The stream body's arguments stay in scalar registers across the stage-1
+        // body (the compiler loads them with the kernel's other arguments at the
+        // start): without a use here it reloads them from the kernel-argument
+        // segment after the barrier below, a memory round trip on the stage-1
+        // waves' way to their suffix windows (0.3-0.5 us per step).
+        asm volatile("" ::"s"(sa.q), "s"(sa.head_off), "s"(sa.scale_log2), "s"(sa.cw_out));
         bar.sync();  // every stage-1 wave is done with the tile ring
     }
     if ((int)blockIdx.x < n2) {
