@@ -187,11 +187,17 @@ struct SuffixArgs {
 // [lo(c), lo(c + 1)). split == 0: P equal chunks, lo(c) = c W / P. split > 0 (P
 // even): chunks 2j and 2j + 1 share the j-th of P / 2 equal ranges, the first
 // taking split / 256 of it (the fused cascade kernel's two roles on one CU).
-// x / d for x >= 0, d > 0: 32-bit division (a dozen instructions) whenever x
-// fits, the 64-bit routine (several times longer) only beyond.
+// floor(x / d) for 0 <= x < 2^52, 1 <= d < 2^31 (here x <= W P with W < 2^31
+// windows and P <= 2^20 chunks) from one IEEE double division: with
+// n = floor(x / d), a quotient that is not the integer n is at most
+// n + 1 - 1 / d, and rounding moves it up by at most (n + 1) 2^-53 < 1 / d
+// (as (n + 1) d <= x + d < 2^53), so it truncates to n; an integer quotient is
+// exact. A 64-bit integer division would expand to a few hundred scalar
+// instructions per use, inline between the hot blocks of the kernels that map
+// windows to chunks (the epilogue was 85% such code and missed the
+// instruction cache on 6% of its fetches).
 __device__ __forceinline__ int64_t div_nonneg(int64_t x, int64_t d) {
-    if (((uint64_t)x >> 32) == 0 && ((uint64_t)d >> 32) == 0) return (int64_t)((uint32_t)x / (uint32_t)d);
-    return x / d;
+    return (int64_t)((double)x / (double)d);
 }
 
 struct ChunkMap {
@@ -1040,11 +1046,19 @@ __device__ __forceinline__ void fold_cut(const float *part_o, const float *part_
         float pl[kB];
         float4 po[kB];
         bool ok[kB];
+        // a chunk with no windows wrote nothing (chunk ca holds the sequence's
+        // start); empty chunks exist only below one window per chunk, and their
+        // test runs as a rolled loop off the common path
+        uint32_t okm = cb - c0 + 1 >= kB ? (1u << kB) - 1 : (1u << (cb - c0 + 1)) - 1;
+        if (!cm.none_empty()) {
+#pragma unroll 1
+            for (int j = 0; j < kB; ++j)
+                if (c0 + j <= cb && c0 + j != ca && cm.empty(c0 + j)) okm &= ~(1u << j);
+        }
 #pragma unroll
         for (int j = 0; j < kB; ++j) {
             const int ch = min(c0 + j, cb);  // clamped: every load is in bounds
-            // a chunk with no windows wrote nothing (chunk ca holds the sequence's start)
-            ok[j] = c0 + j <= cb && (c0 + j == ca || cm.none_empty() || !cm.empty(ch));
+            ok[j] = (okm >> j) & 1;
             const int64_t p = pidx(ch, c0 + j == ca ? 1 : 0);
             pl[j] = part_lse[p];
             po[j] = *reinterpret_cast<const float4 *>(part_o + p * kD + 4 * d4);
