@@ -125,14 +125,15 @@ static_assert(kFusedSplit >= 128 && kFusedSplit < 256, "ChunkMap::none_empty ass
 
 // LDS layout (bytes) of the stream body for G query heads per group and NW waves;
 // STASH (the token-major body) adds the merged results of a phase's segments,
-// held until the phase's window loop is done.
+// held until the phase's window loop is done, and has wider window table entries
+// (plus padding entries past a phase's end, read ahead without a bounds check).
 template <int G, int NW, bool STASH = false>
 struct SfxLds {
     static constexpr int kCw = 0;                                        // int cw[kMaxBatch + 1]
     static constexpr int kLen = ((kMaxBatch + 1) * 4 + 15) / 16 * 16;   // int len[kMaxBatch]
     static constexpr int kWtot = kLen + kMaxBatch * 4;                   // int wtot[NW]
-    static constexpr int kTab = kWtot + 64;                              // int pair tab[kTable]
-    static constexpr int kPw = kTab + kTable * 8;                        // float pw[NW][8][8] p rows
+    static constexpr int kTab = kWtot + 64;  // int pair tab[kTable] (STASH: + 4 padding entries)
+    static constexpr int kPw = kTab + (STASH ? kTable + 4 : kTable) * 8;  // float pw[NW][8][8] p rows
     static constexpr int kQs = kPw + NW * 8 * 8 * 4;                     // bf16 q[kQSlots][G][kD]
     static constexpr int kX = G <= 4 ? 2 : 1;                            // exchange ring slots
     static constexpr int kXo = kQs + kQSlots * G * kD * 2;               // float xo[kX][NW][G][kD]
@@ -275,7 +276,10 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 // query head, which covers the chain's latency; two chains per head cost a
 // second zero-initialised accumulator and an add)
 __device__ __forceinline__ float dot16(const u32x4 &k0, const u32x4 &k1, const u32x4 &q0, const u32x4 &q1) {
-    float d = dot2(k0[0], q0[0], 0.f);
+    // the chain's first product takes its zero as an inline constant (the
+    // compiler materialises the zero in a register for the tied-accumulator form)
+    float d;
+    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(d) : "v"(k0[0]), "v"(q0[0]));
 #pragma unroll
     for (int i = 1; i < 4; ++i) d = dot2(k0[i], q0[i], d);
 #pragma unroll
@@ -320,6 +324,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                                                    const Bar &bar, CK_LDS int *scan_flag = nullptr,
                                                    const CK_LDS char *scan_src = nullptr) {
     static_assert(!TOK || G <= 4, "token-major layout: at most 4 query heads per group");
+    static_assert(!TOK || D + 1 <= 4, "token-major table padding: D + 1 entries past a phase");
     constexpr int NB = D + 1;  // register ring slots: D windows in flight + the one in use
     constexpr int kAcc = TOK ? 16 : 4;  // value accumulators per head and lane
     constexpr int kThr = NW * 64;
@@ -438,8 +443,12 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     const char *kbase = reinterpret_cast<const char *>(a.k) + (int64_t)gk * a.head_off * 2;
     const char *vbase = reinterpret_cast<const char *>(a.v) + (int64_t)gk * a.head_off * 2;
     const int64_t pgb = a.page_stride * 2;
+    const uint32_t pg32 = (uint32_t)pgb, win32 = win_bytes, tok32 = (uint32_t)tokb;  // token-major addressing
 
     float m[G], l[G], acc[G][kAcc];
+    // token-major: m + kTau (the rescale trigger) and the exponent offset (m, 0
+    // while m = -inf), kept beside m: they change only when m does
+    float mt[G], mz[G];
     int nclose = 0;  // segments closed so far (exchange ring position)
     int qslot = 0;   // segment of the current phase
     u32x4 kbuf[NB][2];
@@ -484,24 +493,29 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
 
     // Token-major windows issue their K and V halves at different points of a step
     // (K before the scores, V after the values of the window whose slot it reuses);
-    // both halves address the same rows through the same per-lane offset.
+    // both halves address the same rows through the same per-lane offset. The
+    // table entry holds the window's offset and valid bytes ready for the buffer
+    // descriptor, whose range check returns 0 for the rows of tokens past the
+    // sequence's end (or of an invalid page): a step spends few instructions on
+    // addresses, and the stream wave's instruction count per window is its
+    // critical path.
     struct TokWin {
         int64_t off;
         int range;
-        uint32_t o;
     };
     auto tok_win = [&](i32x2 e) __attribute__((always_inline)) {
         const int page = __builtin_amdgcn_readfirstlane(e[0]);
         const int ey = __builtin_amdgcn_readfirstlane(e[1]);
-        const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
-        return TokWin{(int64_t)(page < 0 ? 0 : page) * pgb + (int64_t)(tab_sub(ey) * kWin) * tokb,
-                      page < 0 ? 0 : (int)win_bytes, t < t1 ? koff : kOob};
+        // 32-bit factors: a page is at most 2^31 bytes (128 tokens x 2^16 heads x
+        // 256 B), a window's offset in its page below that
+        const uint64_t off = (uint64_t)(uint32_t)max(page, 0) * pg32 + (uint32_t)tab_sub(ey) * win32;
+        return TokWin{(int64_t)off, page < 0 ? 0 : (int)(tab_tv(ey) * tok32)};
     };
     auto issue_half = [&](const char *base, const TokWin &w, u32x4 &x0, u32x4 &x1) __attribute__((always_inline)) {
         const __amdgpu_buffer_rsrc_t r =
             __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base + w.off), (short)0, w.range, kRsrcFlags);
-        x0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)w.o, 0, 0));
-        x1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(w.o + 128), 0, 0));
+        x0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)koff, 0, 0));
+        x1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(koff + 128), 0, 0));
     };
 
     // The merged result of sequence b's segment for query head h, dims 4 d4 .. 4 d4
@@ -833,9 +847,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         const int ey = eyr[J];
         const int eyp = eypend;
         eyr[JI] = __builtin_amdgcn_readfirstlane(ei[1]);
-        enext = n + D + 1 < np ? tab[n + D + 1] : i32x2{-1, 0};
-
-        const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
+        enext = tab[n + D + 1];  // at most np + D: a padding entry past the phase
         if (tab_first(ey)) {
             // window n opens a segment: its q rows sit in the slot after the one of
             // the segment window n - 1 may still close
@@ -860,18 +872,24 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 m[h] = -INFINITY;
+                mt[h] = -INFINITY;
+                mz[h] = 0.f;
                 l[h] = 0.f;
 #pragma unroll
                 for (int e = 0; e < kAcc; ++e) acc[h][e] = 0.f;
             }
         }
-        if (t1 < 8) {  // tokens past the sequence's end (all 8 when t1 = 0)
+        {
+            // tokens past the sequence's end (their K rows read as 0; all 8 when t1 = 0)
+            const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
+            if (t1 < 8) {
 #pragma unroll
-            for (int h = 0; h < G; ++h) s[h] = t < t1 ? s[h] : -INFINITY;
+                for (int h = 0; h < G; ++h) s[h] = t < t1 ? s[h] : -INFINITY;
+            }
         }
         bool trig = false;
 #pragma unroll
-        for (int h = 0; h < G; ++h) trig |= s[h] > m[h] + kTau;  // m = -inf: always
+        for (int h = 0; h < G; ++h) trig |= s[h] > mt[h];  // m = -inf: always
         if (__builtin_amdgcn_ballot_w64(trig)) {
 #pragma unroll
             for (int h = 0; h < G; ++h) {
@@ -882,12 +900,14 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                     for (int e = 0; e < kAcc; ++e) acc[h][e] *= f;
                     l[h] *= f;
                     m[h] = m_new;
+                    mt[h] = m_new + kTau;
+                    mz[h] = m_new;
                 }
             }
         }
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            pp[h] = exp2_fast(s[h] - (m[h] == -INFINITY ? 0.f : m[h]));  // 0 for masked tokens
+            pp[h] = exp2_fast(s[h] - mz[h]);  // 0 for masked tokens
             l[h] += pp[h];
         }
       }
@@ -941,7 +961,13 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             p1 = min(p1, cw[bq0 + 64] - w0);  // candidates beyond the 64 examined: the next phase
         }
         const int np = p1 - p0;
-        for (int i = tid; i < np; i += kThr) {
+        // token-major: D + 1 padding entries past the phase (no loads, no tokens)
+        // for the one-step-ahead table reads of its last windows
+        for (int i = tid; i < (TOK ? np + D + 1 : np); i += kThr) {
+            if (TOK && i >= np) {
+                tab[i] = i32x2{-1, 0};
+                continue;
+            }
             const int wg = w0 + p0 + i;
             int b = segb[0], lo_b = seg_lo[0], hi_b = seg_hi[0], len_b = seg_len[0];
 #pragma unroll
@@ -959,19 +985,27 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             const int last = wg == min(hi_b, w1) - 1;
             const int page = a.bt[(int64_t)b * a.bt_cols + k / kWpp];
             const bool ok = page >= 0 && (int64_t)page < a.num_blocks;
-            tab[i] = i32x2{ok ? page : -1, tv | (first << 7) | (last << 8) | ((k % kWpp) << 9) | (b << 11)};
+            const int ey = tv | (first << 7) | (last << 8) | ((k % kWpp) << 9) | (b << 11);
+            tab[i] = i32x2{ok ? page : -1, ey};
         }
         wait_vmcnt<0>();  // q rows and page ids in
         bar.sync();
         qslot = 0;
 #pragma unroll
         for (int j = 0; j < D; ++j) {
-            const i32x2 e = j < np ? tab[j] : i32x2{-1, 0};
-            issue(e, kbuf[j][0], kbuf[j][1], vbuf[j]);
-            if constexpr (TOK) eyr[j] = __builtin_amdgcn_readfirstlane(e[1]);
+            if constexpr (TOK) {
+                const i32x2 e = tab[j];  // j < D: a padding entry when j >= np
+                const TokWin w = tok_win(e);
+                issue_half(kbase, w, kbuf[j][0], kbuf[j][1]);
+                issue_half(vbase, w, vbuf[j][0], vbuf[j][1]);
+                eyr[j] = __builtin_amdgcn_readfirstlane(e[1]);
+            } else {
+                const i32x2 e = j < np ? tab[j] : i32x2{-1, 0};
+                issue(e, kbuf[j][0], kbuf[j][1], vbuf[j]);
+            }
         }
         if constexpr (TOK) {
-            enext = D < np ? tab[D] : i32x2{-1, 0};
+            enext = tab[D];
             // "window -1" of the pipelined step (slot NB - 1): no values, no close;
             // its V slot is zeroed so that p = 0 times it stays 0
 #pragma unroll
