@@ -847,7 +847,6 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         const int ey = eyr[J];
         const int eyp = eypend;
         eyr[JI] = __builtin_amdgcn_readfirstlane(ei[1]);
-        enext = tab[n + D + 1];  // at most np + D: a padding entry past the phase
         if (tab_first(ey)) {
             // window n opens a segment: its q rows sit in the slot after the one of
             // the segment window n - 1 may still close
@@ -858,6 +857,10 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                 qr[h][1] = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2) + 128);
             }
         }
+        // the table entry for the next step, read after the q rows: the score
+        // chains wait for the q rows by the LDS counter, and an earlier read would
+        // be waited for with them
+        enext = tab[n + D + 1];  // at most np + D: a padding entry past the phase
         float s[G];  // scores of window n, then its p
         {
             const u32x4 k0 = kbuf[J][0], k1 = kbuf[J][1];
@@ -883,6 +886,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             // tokens past the sequence's end (their K rows read as 0; all 8 when t1 = 0)
             const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
             if (t1 < 8) {
+                asm volatile("");  // a branch (a sequence's last window), not 8 selects per window
 #pragma unroll
                 for (int h = 0; h < G; ++h) s[h] = t < t1 ? s[h] : -INFINITY;
             }
