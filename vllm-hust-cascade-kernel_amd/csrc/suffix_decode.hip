@@ -594,6 +594,21 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         if (wid == 0 && lane == 0) sb[e] = b;
     };
 
+    // Token-major: the state of a new segment, set at the start and by every close
+    // (a segment opens at the chunk's first window or right after the previous
+    // segment's close); the close's reduction then works on registers it owns.
+    auto reset_seg = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            m[h] = -INFINITY;
+            mt[h] = -INFINITY;
+            mz[h] = 0.f;
+            l[h] = 0.f;
+#pragma unroll
+            for (int e = 0; e < kAcc; ++e) acc[h][e] = 0.f;
+        }
+    };
+
     // Closes segment b (sequence b's windows in this range): folds the lanes' partial
     // sums, hands the wave's (O, m, l) to the exchange ring, and the last wave in
     // merges the NW partials and writes the result (TOK: into the phase's stash).
@@ -708,6 +723,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         }
         ++nclose;
         ++qslot;
+        if constexpr (TOK) reset_seg();
     };
 
     // One window of a phase: issue window n + D into the slot freed last step,
@@ -871,17 +887,6 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         if constexpr (TOK) issue_half(vbase, wi, vbuf[JI][0], vbuf[JI][1]);
         if (tab_last(eyp)) close_seg(tab_b(eyp));
         eypend = ey;
-        if (tab_first(ey)) {
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                m[h] = -INFINITY;
-                mt[h] = -INFINITY;
-                mz[h] = 0.f;
-                l[h] = 0.f;
-#pragma unroll
-                for (int e = 0; e < kAcc; ++e) acc[h][e] = 0.f;
-            }
-        }
         {
             // tokens past the sequence's end (their K rows read as 0; all 8 when t1 = 0)
             const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
@@ -931,6 +936,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     // ---- phases of up to kTable windows and kQSlots segments: table and q rows,
     //      prologue loads, streaming loop --------------------------------------------
     const int nwin = w1 - w0;
+    if constexpr (TOK) reset_seg();  // the chunk's first window opens a segment
     for (int p0 = 0; p0 < nwin;) {
         if (p0 > 0) {
             wait_vmcnt<0>();
