@@ -152,15 +152,19 @@ __device__ __forceinline__ void stage1_wide_body(const Stage1Args &a, CK_LDS cha
         const int tt = (wid * kWBlk + j) * 4 + (lane >> 4);
         dma_off[j] = (uint32_t)(tt * head_stride + g * kD + (((lane & 15) ^ tile_swz(tt)) << 3));
     }
-    // DMAs of tile t (t < ntiles) into ring slot t % 4: the tile's 64 token rows
-    // of K and of V as buffer resources (scalar base), the lane offsets fixed
+    // DMAs of tile t (t < ntiles, page id raw) into ring slot `slot` (t % SLOTS):
+    // the tile's 64 token rows of K and of V as buffer resources (scalar base),
+    // the lane offsets fixed. Byte offsets from 32-bit factors (a page is at most
+    // 2^31 bytes: 128 tokens x 2^16 heads x 256 B), the page id read a barrier
+    // ahead and the slot counted, so the DMA issue is a few scalar instructions.
     const uint32_t tile_bytes = (uint32_t)(kTTok * head_stride * 2);
-    auto issue = [&](int t) {
-        const int raw = __builtin_amdgcn_readfirstlane(s_pages[t >> 1]);
-        const int64_t base = ((int64_t)(raw < 0 ? 0 : raw) * kPage + (t & 1) * kTTok) * head_stride;
-        const ck_rsrc_t rk = buf_rsrc(a.k + base, tile_bytes);
-        const ck_rsrc_t rv = buf_rsrc(a.v + base, tile_bytes);
-        CK_LDS char *kd = smem + (t % SLOTS) * kWStage + wid * kWBlk * 1024;
+    const uint32_t page_bytes = 2 * tile_bytes;
+    auto issue = [&](int t, int raw, int slot) {
+        raw = __builtin_amdgcn_readfirstlane(raw);
+        const uint64_t base = (uint64_t)(uint32_t)max(raw, 0) * page_bytes + ((t & 1) ? tile_bytes : 0u);
+        const ck_rsrc_t rk = buf_rsrc(reinterpret_cast<const char *>(a.k) + base, tile_bytes);
+        const ck_rsrc_t rv = buf_rsrc(reinterpret_cast<const char *>(a.v) + base, tile_bytes);
+        CK_LDS char *kd = smem + slot * kWStage + wid * kWBlk * 1024;
 #pragma unroll
         for (int j = 0; j < kWBlk; ++j) {
             dma16_buf(rk, (int)(dma_off[j] * 2), 0, kd + j * 1024);
@@ -186,8 +190,12 @@ __device__ __forceinline__ void stage1_wide_body(const Stage1Args &a, CK_LDS cha
         return tile_off(t1, d >> 3) + (d & 7) * 2;
     };
 
-    for (int t = 0; t < SLOTS - 1 && t < ntiles; ++t) issue(t);
+    for (int t = 0; t < SLOTS - 1 && t < ntiles; ++t) issue(t, s_pages[t >> 1], t);
+    int slot = 0;  // t % SLOTS
     for (int t = 0; t < ntiles; ++t) {
+        // page ids of tile t and of the tile issued below, read before the waits
+        const int pg_t = s_pages[t >> 1];
+        const int pg_i = t + SLOTS - 1 < ntiles ? s_pages[(t + SLOTS - 1) >> 1] : 0;
         // tile t has landed once at most the DMAs of the tiles after it remain
         const int after = min(SLOTS - 2, ntiles - 1 - t);
         if (after >= 2) wait_vmcnt<4 * kWBlk>();
@@ -195,8 +203,8 @@ __device__ __forceinline__ void stage1_wide_body(const Stage1Args &a, CK_LDS cha
         else wait_vmcnt<0>();
         bar.sync();  // ... in every wave; every wave is done with tile t - 1
         const int nv = min(kTTok, ntok - t * kTTok);
-        const bool ok = s_pages[t >> 1] >= 0;
-        CK_LDS char *kb = smem + (t % SLOTS) * kWStage;
+        const bool ok = pg_t >= 0;
+        CK_LDS char *kb = smem + slot * kWStage;
         CK_LDS char *vb = kb + kTBytes;
         if (nv < kTTok || !ok) {
             // rows past the split's end or of an invalid page: zero them so 0 * V
@@ -209,7 +217,8 @@ __device__ __forceinline__ void stage1_wide_body(const Stage1Args &a, CK_LDS cha
             }
             bar.sync();
         }
-        if (t + SLOTS - 1 < ntiles) issue(t + SLOTS - 1);  // into the slot of tile t - 1
+        if (t + SLOTS - 1 < ntiles) issue(t + SLOTS - 1, pg_i, slot == 0 ? SLOTS - 1 : slot - 1);  // tile t - 1's slot
+        slot = slot == SLOTS - 1 ? 0 : slot + 1;
         if (!wave_active) continue;
 
         // S^T of the two 32-token blocks, K fragments read four ahead
