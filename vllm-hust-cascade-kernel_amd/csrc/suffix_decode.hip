@@ -120,7 +120,7 @@ constexpr int kFusedDepth = 4;
 constexpr int kFusedTokDepth = 2;  // token-major: 16 registers per window and lane
 // Share of each fused workgroup's suffix windows that its streaming waves take
 // (in 1/256); the stage-1 waves take the rest after their stage-1 unit.
-constexpr int kFusedSplit = 192;
+constexpr int kFusedSplit = 176;
 static_assert(kFusedSplit >= 128 && kFusedSplit < 256, "ChunkMap::none_empty assumes a share in [1/2, 1)");
 
 // LDS layout (bytes) of the stream body for G query heads per group and NW waves;
