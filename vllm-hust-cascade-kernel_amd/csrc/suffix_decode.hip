@@ -125,15 +125,14 @@ static_assert(kFusedSplit >= 128 && kFusedSplit < 256, "ChunkMap::none_empty ass
 
 // LDS layout (bytes) of the stream body for G query heads per group and NW waves;
 // STASH (the token-major body) adds the merged results of a phase's segments,
-// held until the phase's window loop is done, and has wider window table entries
-// (plus padding entries past a phase's end, read ahead without a bounds check).
+// held until the phase's window loop is done.
 template <int G, int NW, bool STASH = false>
 struct SfxLds {
     static constexpr int kCw = 0;                                        // int cw[kMaxBatch + 1]
     static constexpr int kLen = ((kMaxBatch + 1) * 4 + 15) / 16 * 16;   // int len[kMaxBatch]
     static constexpr int kWtot = kLen + kMaxBatch * 4;                   // int wtot[NW]
-    static constexpr int kTab = kWtot + 64;  // int pair tab[kTable] (STASH: + 4 padding entries)
-    static constexpr int kPw = kTab + (STASH ? kTable + 4 : kTable) * 8;  // float pw[NW][8][8] p rows
+    static constexpr int kTab = kWtot + 64;               // int pair tab[kTable + 8] (8 padding entries)
+    static constexpr int kPw = kTab + (kTable + 8) * 8;  // float pw[NW][8][8] p rows
     static constexpr int kQs = kPw + NW * 8 * 8 * 4;                     // bf16 q[kQSlots][G][kD]
     static constexpr int kX = G <= 4 ? 2 : 1;                            // exchange ring slots
     static constexpr int kXo = kQs + kQSlots * G * kD * 2;               // float xo[kX][NW][G][kD]
@@ -324,7 +323,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                                                    const Bar &bar, CK_LDS int *scan_flag = nullptr,
                                                    const CK_LDS char *scan_src = nullptr) {
     static_assert(!TOK || G <= 4, "token-major layout: at most 4 query heads per group");
-    static_assert(!TOK || D + 1 <= 4, "token-major table padding: D + 1 entries past a phase");
+    static_assert(D + 1 <= 8, "table padding: D + 1 entries past a phase");
     constexpr int NB = D + 1;  // register ring slots: D windows in flight + the one in use
     constexpr int kAcc = TOK ? 16 : 4;  // value accumulators per head and lane
     constexpr int kThr = NW * 64;
@@ -459,46 +458,18 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     // the 8 G registers cost no occupancy); else q is read from LDS per window
     constexpr bool kQReg = TOK || (G > 4 && NW == kWaves);
     u32x4 qr[kQReg ? G : 1][2];  // this lane's 16 q dims of each head
-    int eyr[NB];               // token-major: packed table fields of the window in each slot
+    int eyr[NB];               // packed table fields of the window in each ring slot
     constexpr int kPwRow = (G + 3) / 4 * 4;  // floats per token in this wave's p rows
     static_assert(kPwRow <= 8, "p row");
     CK_LDS float *pw = (CK_LDS float *)(smem + L::kPw) + wid * 64;
 
-    // K/V loads of the window with table entry e (e[0] < 0: invalid page; a dummy
-    // entry past the phase end has e[1] = 0, no valid tokens) into one ring slot
-    auto issue = [&](i32x2 e, u32x4 &k0, u32x4 &k1, VSlot &vv) __attribute__((always_inline)) {
-        const int page = __builtin_amdgcn_readfirstlane(e[0]);
-        const int ey = __builtin_amdgcn_readfirstlane(e[1]);
-        const int64_t off = (int64_t)(page < 0 ? 0 : page) * pgb + (int64_t)(tab_sub(ey) * kWin) * tokb;
-        const int range = page < 0 ? 0 : (int)win_bytes;
-        const __amdgpu_buffer_rsrc_t rk =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(kbase + off), (short)0, range, kRsrcFlags);
-        const __amdgpu_buffer_rsrc_t rv =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(vbase + off), (short)0, range, kRsrcFlags);
-        const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
-        const uint32_t o = t < t1 ? koff : kOob;
-        k0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)o, 0, 0));
-        k1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)(o + 128), 0, 0));
-        if constexpr (TOK) {
-            vv[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, (int)o, 0, 0));
-            vv[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, (int)(o + 128), 0, 0));
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t ov = 2 * j + hf < t1 ? voff + (uint32_t)(2 * j * tokb) : kOob;
-                vv[j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)ov, 0, 0));
-            }
-        }
-    };
-
-    // Token-major windows issue their K and V halves at different points of a step
-    // (K before the scores, V after the values of the window whose slot it reuses);
-    // both halves address the same rows through the same per-lane offset. The
-    // table entry holds the window's offset and valid bytes ready for the buffer
-    // descriptor, whose range check returns 0 for the rows of tokens past the
-    // sequence's end (or of an invalid page): a step spends few instructions on
-    // addresses, and the stream wave's instruction count per window is its
-    // critical path.
+    // A window's loads: the buffer descriptor of its rows (K or V) starts at the
+    // window and spans its valid tokens, so the range check returns 0 for the rows
+    // of tokens past the sequence's end (or of an invalid page: range 0) and the
+    // lane offsets are constants. The offset from 32-bit factors: a page is at most
+    // 2^31 bytes (128 tokens x 2^16 heads x 256 B), a window's offset in its page
+    // below that. A step spends few instructions on addresses: the stream wave's
+    // instruction count per window is its critical path.
     struct TokWin {
         int64_t off;
         int range;
@@ -506,11 +477,33 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     auto tok_win = [&](i32x2 e) __attribute__((always_inline)) {
         const int page = __builtin_amdgcn_readfirstlane(e[0]);
         const int ey = __builtin_amdgcn_readfirstlane(e[1]);
-        // 32-bit factors: a page is at most 2^31 bytes (128 tokens x 2^16 heads x
-        // 256 B), a window's offset in its page below that
         const uint64_t off = (uint64_t)(uint32_t)max(page, 0) * pg32 + (uint32_t)tab_sub(ey) * win32;
         return TokWin{(int64_t)off, page < 0 ? 0 : (int)(tab_tv(ey) * tok32)};
     };
+
+    // K/V loads of the window with table entry e (e[0] < 0: invalid page; a padding
+    // entry past the phase end reads nothing) into one ring slot
+    auto issue = [&](i32x2 e, u32x4 &k0, u32x4 &k1, VSlot &vv) __attribute__((always_inline)) {
+        const TokWin w = tok_win(e);
+        const __amdgpu_buffer_rsrc_t rk =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(kbase + w.off), (short)0, w.range, kRsrcFlags);
+        const __amdgpu_buffer_rsrc_t rv =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(vbase + w.off), (short)0, w.range, kRsrcFlags);
+        k0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)koff, 0, 0));
+        k1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)(koff + 128), 0, 0));
+        if constexpr (TOK) {
+            vv[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, (int)koff, 0, 0));
+            vv[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, (int)(koff + 128), 0, 0));
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                vv[j] = __builtin_bit_cast(
+                    u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)(voff + (uint32_t)(2 * j * tokb)), 0, 0));
+        }
+    };
+
+    // Token-major windows issue their K and V halves at different points of a step
+    // (K before the scores, V after the values of the window whose slot it reuses).
     auto issue_half = [&](const char *base, const TokWin &w, u32x4 &x0, u32x4 &x1) __attribute__((always_inline)) {
         const __amdgpu_buffer_rsrc_t r =
             __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base + w.off), (short)0, w.range, kRsrcFlags);
@@ -726,17 +719,18 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         if constexpr (TOK) reset_seg();
     };
 
+    i32x2 enext = i32x2{-1, 0};  // the table entry of the next window to issue
     // One window of a phase: issue window n + D into the slot freed last step,
     // compute window n from slot J = n % NB, close its segment if it ends here.
     auto step = [&](auto jc, int n, int np) __attribute__((always_inline)) {
       if constexpr (!TOK) {
         constexpr int J = decltype(jc)::value;
         constexpr int JI = (J + D) % NB;  // slot of window n + D (freed by window n - 1)
-        const int ni = n + D;
-        const i32x2 ei = ni < np ? tab[ni] : i32x2{-1, 0};
+        const i32x2 ei = enext;           // tab[n + D], read a step ahead
         issue(ei, kbuf[JI][0], kbuf[JI][1], vbuf[JI]);
-
-        const int ey = __builtin_amdgcn_readfirstlane(tab[n][1]);
+        eyr[JI] = __builtin_amdgcn_readfirstlane(ei[1]);
+        const int ey = eyr[J];
+        enext = tab[n + D + 1];  // at most np + D: a padding entry past the phase
         const int b = tab_b(ey);
         const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
         const CK_LDS char *qrow = qs + qslot * G * (kD * 2) + c * 16;
@@ -832,7 +826,6 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     // softmax. The table entry of the window to issue was read one step ahead and
     // the packed fields of each window travel in the ring with its data, so the
     // step's only LDS access is off its critical path.
-    i32x2 enext = i32x2{-1, 0};
     float pp[G];     // p of window n - 1 (0 before a phase's first window)
     int eypend = 0;  // packed table fields of window n - 1
     auto pv_tok = [&](const float *p, const VSlot &vv) __attribute__((always_inline)) {
@@ -971,10 +964,10 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             p1 = min(p1, cw[bq0 + 64] - w0);  // candidates beyond the 64 examined: the next phase
         }
         const int np = p1 - p0;
-        // token-major: D + 1 padding entries past the phase (no loads, no tokens)
-        // for the one-step-ahead table reads of its last windows
-        for (int i = tid; i < (TOK ? np + D + 1 : np); i += kThr) {
-            if (TOK && i >= np) {
+        // D + 1 padding entries past the phase (no loads, no tokens) for the
+        // one-step-ahead table reads of its last windows
+        for (int i = tid; i < np + D + 1; i += kThr) {
+            if (i >= np) {
                 tab[i] = i32x2{-1, 0};
                 continue;
             }
@@ -1010,10 +1003,12 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                 issue_half(vbase, w, vbuf[j][0], vbuf[j][1]);
                 eyr[j] = __builtin_amdgcn_readfirstlane(e[1]);
             } else {
-                const i32x2 e = j < np ? tab[j] : i32x2{-1, 0};
+                const i32x2 e = tab[j];  // j < D: a padding entry when j >= np
                 issue(e, kbuf[j][0], kbuf[j][1], vbuf[j]);
+                eyr[j] = __builtin_amdgcn_readfirstlane(e[1]);
             }
         }
+        if constexpr (!TOK) enext = tab[D];
         if constexpr (TOK) {
             enext = tab[D];
             // "window -1" of the pipelined step (slot NB - 1): no values, no close;
