@@ -1341,7 +1341,14 @@ __global__ __launch_bounds__(512) void cascade_fused_kernel(s1::Stage1Args s1a, 
         bar.sync();  // every stage-1 wave is done with the tile ring
     }
     if ((int)blockIdx.x < n2) {
-        const int g = (int)blockIdx.x % sa.kv_heads, j = (int)blockIdx.x / sa.kv_heads;
+        // The stream roles take kv head group blockIdx + 3 (mod kv_heads) while the
+        // stage-1 unit order puts kv head x on XCD x (blockIdx % 8) at the usual
+        // shapes: a workgroup's two roles then read different kv heads. Pages of
+        // some kv heads are slower to fetch than others (by their address bits: up
+        // to ~15% measured), and with both roles on one head their slowness stacked
+        // on the same workgroups, which set the kernel's end (1.1-1.6 us per step).
+        constexpr int kRoleRot = 3;
+        const int g = ((int)blockIdx.x + kRoleRot) % sa.kv_heads, j = (int)blockIdx.x / sa.kv_heads;
         // the streaming waves scan the lengths; the stage-1 waves reuse that scan
         suffix_stream_body<G, 4, (G <= 4 ? kFusedTokDepth : kFusedDepth), (G <= 4)>(
             sa, smem + (role ? 0 : kFusedS1Lds), (2 * j + role) * sa.kv_heads + g, threadIdx.x & 255, bar, bars + 4,
