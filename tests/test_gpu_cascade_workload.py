@@ -177,7 +177,7 @@ def test_suffix_benchmark_workload_bit_stable():
                L_ref, "oracle")
 
 
-def fused_chunk_segments(suf, kv_groups, split=176):
+def fused_chunk_segments(suf, kv_groups, split=208):
     """Most sequences any fused chunk holds (host restatement of the kernel's chunk
     map: 32-token windows, 256 / kv_groups chunk pairs per kv head group, the first
     chunk of a pair taking split / 256 of the pair's windows)."""

@@ -1,5 +1,6 @@
 // suffix_decode.hip - per-sequence paged decode attention over each sequence's
-// own suffix pages (cascade stage 2) on gfx950, without MFMA.
+// own suffix pages (cascade stage 2) on gfx950: the stand-alone op on the
+// vector ALU, the fused cascade's streaming waves on the matrix cores.
 //
 // Role: replaces the closed CANN op npu_fused_infer_attention_score_v2 the
 // reference calls for stage 2 (ascend-kernel/README.md:186-197): one query
@@ -8,8 +9,9 @@
 // yields O = 0, LSE = -inf, which the merge treats as weight 0.
 //
 // Arithmetic: S = q k^T * scale in fp32, online softmax in the log2 domain,
-// fp32 P and fp32 accumulation (no bf16 rounding of P: there is no matrix
-// core here to feed), O = acc / l, LSE = ln(l) + max.
+// fp32 P and fp32 accumulation (no bf16 rounding of P; the matrix-core body
+// feeds P as two bf16 terms whose sum is P within 2^-16), O = acc / l,
+// LSE = ln(l) + max.
 //
 // MI355X design: HBM-bound streaming with a persistent, balanced grid, and as
 // little vector-ALU work per byte as the arithmetic allows (a wave64 vector
@@ -62,7 +64,8 @@
 //   its slowest wave.)
 // * Cascade (stage 1 + suffix + merge): one fused kernel, one workgroup per CU.
 //   Waves 0-3 run the stage-1 body (MFMA, LDS tiles: matrix cores and LDS),
-//   waves 4-7 stream suffix windows (memory pipe and vector ALU); each role
+//   waves 4-7 stream suffix windows (memory pipe; their 4-head groups on the
+//   matrix cores, with one LDS round trip per window to transpose V); each role
 //   synchronises only its own four waves through an LDS counter barrier, so
 //   the two run side by side instead of one kernel after the other, and a
 //   small epilogue kernel merges the two results.
@@ -117,16 +120,19 @@ constexpr int kRsrcFlags = 0x00020000;  // buffer descriptor word 3 for gfx9 raw
 // kernel, whose 4 streaming waves per CU carry the CU's whole share.
 constexpr int kDepth = 1;
 constexpr int kFusedDepth = 4;
-constexpr int kFusedTokDepth = 2;  // token-major: 16 registers per window and lane
+constexpr int kFusedTokDepth = 2;  // token-major (matrix-core body: 24 registers per window and lane; 3, 4 slower)
 // Share of each fused workgroup's suffix windows that its streaming waves take
 // (in 1/256); the stage-1 waves take the rest after their stage-1 unit.
-constexpr int kFusedSplit = 176;
+constexpr int kFusedSplit = 208;
 static_assert(kFusedSplit >= 128 && kFusedSplit < 256, "ChunkMap::none_empty assumes a share in [1/2, 1)");
 
 // LDS layout (bytes) of the stream body for G query heads per group and NW waves;
 // STASH (the token-major body) adds the merged results of a phase's segments,
-// held until the phase's window loop is done.
-template <int G, int NW, bool STASH = false>
+// held until the phase's window loop is done; MF (the matrix-core body) adds
+// each wave's V transpose slot: 8 token rows of 256 bytes at a 288-byte pitch
+// (the pitch puts the 4 rows of a transpose read in distinct bank groups).
+constexpr int kVtPitch = 288;
+template <int G, int NW, bool STASH = false, bool MF = false>
 struct SfxLds {
     static constexpr int kCw = 0;                                        // int cw[kMaxBatch + 1]
     static constexpr int kLen = ((kMaxBatch + 1) * 4 + 15) / 16 * 16;   // int len[kMaxBatch]
@@ -142,7 +148,8 @@ struct SfxLds {
     static constexpr int kSo = (kBar + 8 + 15) / 16 * 16;                // float so[kQSlots][G][kD] (STASH)
     static constexpr int kSl = kSo + (STASH ? kQSlots * G * kD * 4 : 0); // float sl[kQSlots][G]
     static constexpr int kSb = kSl + (STASH ? kQSlots * G * 4 : 0);      // int sb[kQSlots]
-    static constexpr int kBytes = (kSb + (STASH ? kQSlots * 4 : 0) + 15) / 16 * 16;
+    static constexpr int kVt = (kSb + (STASH ? kQSlots * 4 : 0) + 15) / 16 * 16;  // char vt[NW][8][kVtPitch] (MF)
+    static constexpr int kBytes = kVt + (MF ? NW * 8 * kVtPitch : 0);
     static_assert(kTab % 16 == 0 && kPw % 16 == 0 && kQs % 16 == 0 && kXo % 16 == 0 && kXml % 8 == 0 &&
                       kSo % 16 == 0,
                   "aligned LDS rows");
@@ -314,22 +321,41 @@ __device__ __forceinline__ int64_t clamp_len(const SuffixArgs &a, int64_t kvl) {
 //   of the merging wave would also wait for its acknowledgement (or for loads
 //   issued after it), a stall of about a round trip per merge.
 //
+// MF (with TOK: the same table, segments, exchange ring and stash) computes a
+// window on the matrix cores instead of the vector ALU; a wave still owns 8
+// tokens of every window, and lane (g, n) = (lane / 16, lane % 16):
+// * S^T = K q^T on v_mfma_f32_16x16x32_bf16: A = K, row n = token n of the wave's
+//   8 (rows 8-15 read nothing: zeros), dims 32 s + 8 g .. + 7 at step s, straight
+//   from global memory; B = q of head n, the same dims. The result puts token
+//   4 g + r, head n in register r of lane (g, n); lanes of rows 8-15 (g >= 2) and
+//   of heads n >= G get score -inf through the scale's addend, hence p = 0.
+// * O^T += V^T P^T on v_mfma_f32_16x16x16_bf16, one 16-dim tile of O per MFMA: B =
+//   P^T is the score layout itself (lane (g, n): tokens 4 g .. 4 g + 3 of head n),
+//   and A = V^T comes from the V rows through the wave's LDS slot by
+//   ds_read_b64_tr_b16 (lane (g, n): dim n of the tile, tokens 4 g .. 4 g + 3).
+//   P enters as two bf16 terms, hi = p truncated and lo = p - hi rounded (|p - hi|
+//   < 2^-7 p, so p = hi + lo within 2^-16 p): fp32 P for the arithmetic's purposes.
+// * The softmax state of head n sits in lane (g, n), the same for every g: the
+//   running max is reduced over the 4 groups when it moves, the row sum when the
+//   segment closes, and O^T needs no reduction (the MFMA summed the tokens).
+//
 // Two bodies on one CU may share one scan: the body given scan_src (the other
 // body's LDS) skips its own, waits until scan_flag is set and reads the other's
 // lengths and window prefix sums; the body given only scan_flag sets it once its
 // scan is complete.
-template <int G, int NW, int D, bool TOK, class Bar>
+template <int G, int NW, int D, bool TOK, bool MF, class Bar>
 __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS char *smem, int lb, int tid,
                                                    const Bar &bar, CK_LDS int *scan_flag = nullptr,
                                                    const CK_LDS char *scan_src = nullptr) {
     static_assert(!TOK || G <= 4, "token-major layout: at most 4 query heads per group");
+    static_assert(!MF || (TOK && NW == 4), "the matrix-core body runs on the token-major machinery, 4 waves");
     static_assert(D + 1 <= 8, "table padding: D + 1 entries past a phase");
     constexpr int NB = D + 1;  // register ring slots: D windows in flight + the one in use
     constexpr int kAcc = TOK ? 16 : 4;  // value accumulators per head and lane
     constexpr int kThr = NW * 64;
     constexpr int kWin = 8 * NW;         // tokens per window
     constexpr int kWpp = kPage / kWin;   // windows per page
-    using L = SfxLds<G, NW, TOK>;
+    using L = SfxLds<G, NW, TOK, MF>;
     CK_LDS int *cw = (CK_LDS int *)((scan_src ? scan_src : smem) + L::kCw);
     CK_LDS int *len = (CK_LDS int *)((scan_src ? scan_src : smem) + L::kLen);
     CK_LDS int *wtot = (CK_LDS int *)(smem + L::kWtot);
@@ -443,14 +469,31 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     const char *vbase = reinterpret_cast<const char *>(a.v) + (int64_t)gk * a.head_off * 2;
     const int64_t pgb = a.page_stride * 2;
     const uint32_t pg32 = (uint32_t)pgb, win32 = win_bytes, tok32 = (uint32_t)tokb;  // token-major addressing
+    // matrix-core body: lane (mg, mn); its K rows (token 8 wid + mn, 16 bytes at
+    // 64 s + 16 mg for step s; rows 8-15 read nothing), its V bytes in the wave's
+    // LDS slot (written by lane (t, c), read back transposed: tile T at + 32 T) and
+    // the addend of its scores (-inf: a padding row or head)
+    const int mn = lane & 15, mg = lane >> 4;
+    const uint32_t kmoff = mn < 8 ? (uint32_t)((8 * wid + mn) * tokb + 16 * mg) : kOob;
+    CK_LDS char *vt = smem + L::kVt + wid * 8 * kVtPitch;
+    const int vwo = t * kVtPitch + 16 * c;
+    const int vro = (4 * (mg & 1) + (mn >> 2)) * kVtPitch + 8 * (mn & 3);
+    const float sbias = (mg < 2 && mn < G) ? 0.f : -INFINITY;
 
     float m[G], l[G], acc[G][kAcc];
     // token-major: m + kTau (the rescale trigger) and the exponent offset (m, 0
     // while m = -inf), kept beside m: they change only when m does
     float mt[G], mz[G];
+    // matrix-core body: the O^T tiles (dims 16 T + 4 mg + r of head mn), head mn's
+    // softmax state (m, m + kTau, the exponent offset, this lane's share of the
+    // row sum), q fragments, and the P^T operand (hi, lo) of the pending window
+    f32x4 oacc[8];
+    float m1, mt1, mz1, l1;
+    u32x4 qf[4];
+    uint32_t ph[2], pl[2];
     int nclose = 0;  // segments closed so far (exchange ring position)
     int qslot = 0;   // segment of the current phase
-    u32x4 kbuf[NB][2];
+    u32x4 kbuf[NB][MF ? 4 : 2];
     using VSlot = std::conditional_t<TOK, u32x4[2], u32x2[4]>;
     VSlot vbuf[NB];
     // q in registers from the window that opens a segment: the token-major body,
@@ -500,6 +543,15 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                 vv[j] = __builtin_bit_cast(
                     u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, (int)(voff + (uint32_t)(2 * j * tokb)), 0, 0));
         }
+    };
+
+    // matrix-core body: a window's K rows as the 4 A fragments of its score MFMAs
+    auto issue_kmf = [&](const TokWin &w, u32x4 *kf) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t r =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(kbase + w.off), (short)0, w.range, kRsrcFlags);
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+            kf[s4] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(kmoff + 64 * s4), 0, 0));
     };
 
     // Token-major windows issue their K and V halves at different points of a step
@@ -591,6 +643,15 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     // (a segment opens at the chunk's first window or right after the previous
     // segment's close); the close's reduction then works on registers it owns.
     auto reset_seg = [&]() __attribute__((always_inline)) {
+        if constexpr (MF) {
+            m1 = -INFINITY;
+            mt1 = -INFINITY;
+            mz1 = 0.f;
+            l1 = 0.f;
+#pragma unroll
+            for (int T = 0; T < 8; ++T) oacc[T] = f32x4{0.f, 0.f, 0.f, 0.f};
+            return;
+        }
 #pragma unroll
         for (int h = 0; h < G; ++h) {
             m[h] = -INFINITY;
@@ -613,9 +674,16 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         // with head 2 s5 + s4, all 16 of its dims, in 112 instructions instead of
         // 320 for summing every accumulator over all 8 slots.
         float f2[16];
+        float lt1 = 0.f;  // matrix-core body: head mn's row sum over the 4 groups
+        if constexpr (MF) {
+            lt1 = sum_xor32(sum_xor16(l1));
+        } else {
 #pragma unroll
-        for (int h = 0; h < G; ++h) l[h] = sum_slots(l[h]);
-        if constexpr (TOK && G == 4) {
+            for (int h = 0; h < G; ++h) l[h] = sum_slots(l[h]);
+        }
+        if constexpr (MF) {
+            // O^T needs no reduction: the MFMAs summed over the tokens
+        } else if constexpr (TOK && G == 4) {
             float f1[32];
 #pragma unroll
             for (int j = 0; j < 32; ++j) {
@@ -653,7 +721,17 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         }
         CK_LDS float *xo_r = xo + r * NW * G * kD;
         CK_LDS float *xml_r = xml + r * NW * G * 2;
-        if constexpr (TOK && G == 4) {
+        if constexpr (MF) {
+            if (mn < G) {
+#pragma unroll
+                for (int T = 0; T < 8; ++T)
+                    *reinterpret_cast<CK_LDS f32x4 *>(xo_r + (wid * G + mn) * kD + 16 * T + 4 * mg) = oacc[T];
+                if (mg == 0) {
+                    xml_r[(wid * G + mn) * 2] = m1;
+                    xml_r[(wid * G + mn) * 2 + 1] = lt1;
+                }
+            }
+        } else if constexpr (TOK && G == 4) {
             if ((lane & 8) == 0) {
                 CK_LDS float *dst = xo_r + (wid * G + (lane >> 4)) * kD + 8 * c;
                 *reinterpret_cast<CK_LDS f32x4 *>(dst) = f32x4{f2[0], f2[1], f2[2], f2[3]};
@@ -681,7 +759,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                 *reinterpret_cast<CK_LDS f32x4 *>(xo_r + (wid * G + h) * kD + 4 * dd) =
                     f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
         }
-        if (lane == 0) {
+        if (!MF && lane == 0) {
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 xml_r[(wid * G + h) * 2] = m[h];
@@ -914,13 +992,118 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         }
       }
     };
+    // Matrix-core values of the pending window: its V rows (lane (t, c) holds 32
+    // bytes of token t) into the wave's LDS slot, back as the V^T fragments of the 8
+    // dim tiles, then O^T += V^T P^T for the hi and the lo term of P. The slot is
+    // written and read by this wave only, whose LDS operations run in issue order.
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    auto pv_mf = [&](const VSlot &vv) __attribute__((always_inline)) {
+      if constexpr (MF) {
+        *reinterpret_cast<CK_LDS u32x4 *>(vt + vwo) = vv[0];
+        *reinterpret_cast<CK_LDS u32x4 *>(vt + vwo + 128) = vv[1];
+        uint2 vtf[8];
+#pragma unroll
+        for (int T = 0; T < 8; ++T) vtf[T] = lds_read_tr16(vt + vro + 32 * T);
+        const s16x4 bh = __builtin_bit_cast(s16x4, uint2{ph[0], ph[1]});
+        const s16x4 bl = __builtin_bit_cast(s16x4, uint2{pl[0], pl[1]});
+#pragma unroll
+        for (int T = 0; T < 8; ++T) {
+            const s16x4 av = __builtin_bit_cast(s16x4, vtf[T]);
+            oacc[T] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bh, oacc[T], 0, 0, 0);
+            oacc[T] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bl, oacc[T], 0, 0, 0);
+        }
+      }
+    };
+    // Matrix-core window step, pipelined like the token-major one: step n issues
+    // window n + D's K rows, computes window n's scores, then window n - 1's values
+    // (its P kept from the step before, its V rows still in their ring slot),
+    // issues window n + D's V rows into that slot, closes window n - 1's segment if
+    // it ends there and finishes window n's softmax.
+    auto step_mf = [&](auto jc, int n, int np) __attribute__((always_inline)) {
+      if constexpr (MF) {
+        constexpr int J = decltype(jc)::value;
+        constexpr int JI = (J + D) % NB;  // window n + D, into the slot of window n - 1
+        const i32x2 ei = enext;
+        const TokWin wi = tok_win(ei);
+        issue_kmf(wi, kbuf[JI]);
+        const int ey = eyr[J];
+        const int eyp = eypend;
+        eyr[JI] = __builtin_amdgcn_readfirstlane(ei[1]);
+        if (tab_first(ey)) {
+            // window n opens a segment: q of head mn (heads past G: any finite row,
+            // their scores are -inf), in the slot after the segment window n - 1
+            // may still close
+            const CK_LDS char *qrow =
+                qs + ((qslot + (tab_last(eyp) ? 1 : 0)) * G + (mn < G ? mn : 0)) * (kD * 2) + 16 * mg;
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) qf[s4] = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + 64 * s4);
+        }
+        enext = tab[n + D + 1];  // at most np + D: a padding entry past the phase
+        f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kbuf[J][s4]),
+                                                         __builtin_bit_cast(bf16x8, qf[s4]), sc, 0, 0, 0);
+        pv_mf(vbuf[JI]);
+        issue_half(vbase, wi, vbuf[JI][0], vbuf[JI][1]);
+        if (tab_last(eyp)) close_seg(tab_b(eyp));
+        eypend = ey;
+        float s[4];  // scores of tokens 4 mg + r, head mn; then p
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[r] = fmaf(sc[r], a.scale_log2, sbias);
+        {
+            const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
+            if (t1 < 8) {
+                asm volatile("");  // a branch (a sequence's last window)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s[r] = 4 * mg + r < t1 ? s[r] : -INFINITY;
+            }
+        }
+        bool trig = false;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) trig |= s[r] > mt1;  // m = -inf: any real score
+        if (__builtin_amdgcn_ballot_w64(trig)) {
+            // head mn's max over its 8 tokens (the 4 groups), the same in its 4 lanes
+            const float x = max_xor32(max_xor16(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]))));
+            if (x > m1) {
+                const float f = exp2_fast(m1 - x);  // 0 from -inf
+#pragma unroll
+                for (int T = 0; T < 8; ++T) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) oacc[T][r] *= f;
+                }
+                l1 *= f;
+                m1 = x;
+                mt1 = x + kTau;
+                mz1 = x;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            s[r] = exp2_fast(s[r] - mz1);  // 0 for masked tokens and padding lanes
+            l1 += s[r];
+        }
+        // P^T of window n for the next step: hi = p truncated to bf16 (exact in fp32),
+        // lo = p - hi (exact) rounded to bf16
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t u0 = __float_as_uint(s[2 * i]), u1 = __float_as_uint(s[2 * i + 1]);
+            ph[i] = __builtin_amdgcn_perm(u1, u0, 0x07060302u);
+            pl[i] = pack_bf16x2(s[2 * i] - __uint_as_float(u0 & 0xFFFF0000u),
+                                s[2 * i + 1] - __uint_as_float(u1 & 0xFFFF0000u));
+        }
+      }
+    };
     // after a phase's last window (np - 1, in slot (np - 1) % NB): its values and
     // its segment's close
     auto drain_tok = [&](int np) __attribute__((always_inline)) {
       if constexpr (TOK) {
         const int js = (np - 1) % NB;  // wave-uniform
         static_for<NB>([&](auto jc) __attribute__((always_inline)) {
-            if (js == decltype(jc)::value) pv_tok(pp, vbuf[decltype(jc)::value]);
+            if (js == decltype(jc)::value) {
+                if constexpr (MF) pv_mf(vbuf[decltype(jc)::value]);
+                else pv_tok(pp, vbuf[decltype(jc)::value]);
+            }
         });
         if (tab_last(eypend)) close_seg(tab_b(eypend));
       }
@@ -999,7 +1182,8 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             if constexpr (TOK) {
                 const i32x2 e = tab[j];  // j < D: a padding entry when j >= np
                 const TokWin w = tok_win(e);
-                issue_half(kbase, w, kbuf[j][0], kbuf[j][1]);
+                if constexpr (MF) issue_kmf(w, kbuf[j]);
+                else issue_half(kbase, w, kbuf[j][0], kbuf[j][1]);
                 issue_half(vbase, w, vbuf[j][0], vbuf[j][1]);
                 eyr[j] = __builtin_amdgcn_readfirstlane(e[1]);
             } else {
@@ -1015,6 +1199,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             // its V slot is zeroed so that p = 0 times it stays 0
 #pragma unroll
             for (int h = 0; h < G; ++h) pp[h] = 0.f;
+            ph[0] = ph[1] = pl[0] = pl[1] = 0u;
             vbuf[NB - 1][0] = u32x4{0u, 0u, 0u, 0u};
             vbuf[NB - 1][1] = u32x4{0u, 0u, 0u, 0u};
             eypend = 0;
@@ -1025,7 +1210,8 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         int n = 0;
         for (int it = np / NB; it > 0; --it) {
             static_for<NB>([&](auto jc) __attribute__((always_inline)) {
-                if constexpr (TOK) step_tok(jc, n + decltype(jc)::value, np);
+                if constexpr (MF) step_mf(jc, n + decltype(jc)::value, np);
+                else if constexpr (TOK) step_tok(jc, n + decltype(jc)::value, np);
                 else step(jc, n + decltype(jc)::value, np);
             });
             n += NB;
@@ -1033,7 +1219,8 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         const int rem = np - n;
         static_for<NB>([&](auto jc) __attribute__((always_inline)) {
             if (decltype(jc)::value < rem) {
-                if constexpr (TOK) step_tok(jc, n + decltype(jc)::value, np);
+                if constexpr (MF) step_mf(jc, n + decltype(jc)::value, np);
+                else if constexpr (TOK) step_tok(jc, n + decltype(jc)::value, np);
                 else step(jc, n + decltype(jc)::value, np);
             }
         });
@@ -1060,12 +1247,12 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
 template <int G>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void suffix_stream_kernel(SuffixArgs a) {
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-    suffix_stream_body<G, kWaves, kDepth, false>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
+    suffix_stream_body<G, kWaves, kDepth, false, false>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
 }
 template <int G>
 __global__ __launch_bounds__(kThreads) void suffix_stream_wide_kernel(SuffixArgs a) {
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-    suffix_stream_body<G, kWaves, kDepth, false>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
+    suffix_stream_body<G, kWaves, kDepth, false, false>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
 }
 
 // Folds the partials of one query head of a sequence cut by chunk boundaries
@@ -1311,8 +1498,11 @@ __global__ __launch_bounds__(kMaxGroup * 32) void cascade_epilogue_kernel(Epilog
 // waves finish. Each role has its own LDS region and barrier; neither waits
 // for the other.
 constexpr int kFusedS1Lds = s1::wide_lds_bytes<3>();
+// the stream body on 4 waves: token-major windows on the matrix cores up to 4 heads
 template <int G>
-using FusedSfx = SfxLds<G, 4, (G <= 4)>;  // the stream body's layout on 4 waves (token-major up to 4 heads)
+constexpr bool kFusedMf = G <= 4;
+template <int G>
+using FusedSfx = SfxLds<G, 4, (G <= 4), kFusedMf<G>>;
 template <int G>
 constexpr int fused_lds_bytes() { return kFusedS1Lds + FusedSfx<G>::kBytes + 32; }
 static_assert(fused_lds_bytes<4>() <= 160 * 1024 && fused_lds_bytes<kMaxGroup>() <= 160 * 1024,
@@ -1350,7 +1540,7 @@ __global__ __launch_bounds__(512) void cascade_fused_kernel(s1::Stage1Args s1a, 
         constexpr int kRoleRot = 3;
         const int g = ((int)blockIdx.x + kRoleRot) % sa.kv_heads, j = (int)blockIdx.x / sa.kv_heads;
         // the streaming waves scan the lengths; the stage-1 waves reuse that scan
-        suffix_stream_body<G, 4, (G <= 4 ? kFusedTokDepth : kFusedDepth), (G <= 4)>(
+        suffix_stream_body<G, 4, (G <= 4 ? kFusedTokDepth : kFusedDepth), (G <= 4), kFusedMf<G>>(
             sa, smem + (role ? 0 : kFusedS1Lds), (2 * j + role) * sa.kv_heads + g, threadIdx.x & 255, bar, bars + 4,
             role ? smem + kFusedS1Lds : nullptr);
     }
