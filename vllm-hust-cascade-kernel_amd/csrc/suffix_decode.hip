@@ -1254,6 +1254,17 @@ __global__ __launch_bounds__(kThreads) void suffix_stream_wide_kernel(SuffixArgs
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
     suffix_stream_body<G, kWaves, kDepth, false, false>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
 }
+// Up to 4 query heads per group on the matrix cores: the fused kernel's streaming
+// body on 4 waves, two workgroups per CU (its LDS: 64 KB each).
+template <int G>
+constexpr bool kSuffixMf = G <= 4;
+template <int G>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void suffix_stream_mf_kernel(SuffixArgs a) {
+    extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+    suffix_stream_body<G, 4, kFusedTokDepth, true, true>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x,
+                                                         WgBarrier{});
+}
+static_assert(SfxLds<4, 4, true, true>::kBytes <= 80 * 1024, "two matrix-core stream workgroups per CU");
 
 // Folds the partials of one query head of a sequence cut by chunk boundaries
 // (chunks ca < cb): the tail slot (1) of chunk ca and the head slot (0) of every
@@ -1571,13 +1582,17 @@ int launch_fused(const s1::Stage1Args &s1a, int64_t n1, const SuffixArgs &a, con
 template <int G>
 int launch_suffix(const SuffixArgs &a, bool fixup, const EpilogueArgs *epi, hipStream_t st) {
     static std::atomic<uint64_t> lds_set{0};
-    constexpr int kLds = SfxLds<G, kWaves>::kBytes;
+    constexpr int kLds = kSuffixMf<G> ? SfxLds<G, 4, true, true>::kBytes : SfxLds<G, kWaves>::kBytes;
     const void *fn;
-    if constexpr (G <= 4) fn = reinterpret_cast<const void *>(&suffix_stream_kernel<G>);
+    if constexpr (kSuffixMf<G>) fn = reinterpret_cast<const void *>(&suffix_stream_mf_kernel<G>);
+    else if constexpr (G <= 4) fn = reinterpret_cast<const void *>(&suffix_stream_kernel<G>);
     else fn = reinterpret_cast<const void *>(&suffix_stream_wide_kernel<G>);
     int rc = ensure_dynamic_lds(fn, kLds, lds_set);
     if (rc != CK_OK) return rc;
-    if constexpr (G <= 4)
+    if constexpr (kSuffixMf<G>)
+        hipLaunchKernelGGL(suffix_stream_mf_kernel<G>, dim3((unsigned)(a.kv_heads * a.chunks)), dim3(256), kLds, st,
+                           a);
+    else if constexpr (G <= 4)
         hipLaunchKernelGGL(suffix_stream_kernel<G>, dim3((unsigned)(a.kv_heads * a.chunks)), dim3(kThreads), kLds,
                            st, a);
     else
