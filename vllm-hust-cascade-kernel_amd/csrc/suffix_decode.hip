@@ -114,42 +114,43 @@ constexpr float kTau = 8.0f;        // log2 headroom before the running max move
 constexpr uint32_t kOob = 0x80000000u;  // a buffer offset past every window's range
 constexpr int kRsrcFlags = 0x00020000;  // buffer descriptor word 3 for gfx9 raw loads
 
-// windows of loads in flight per wave: one in the stand-alone kernel (16 waves
-// per CU: 64 KB per CU, about the amount the memory system serves best; deeper
-// rings of 2-10 windows measured slower there), more in the fused cascade
-// kernel, whose 4 streaming waves per CU carry the CU's whole share.
+// windows of loads in flight per wave: dims-major, one in the stand-alone wide
+// kernel (deeper rings of 2-10 windows measured slower in its 16-wave-per-CU
+// form) and 4 in the fused cascade kernel, whose 4 streaming waves per CU carry
+// the CU's whole share; token-major, 2 (24 registers per window and lane; 3 and
+// 4 measured slower in the fused kernel).
 constexpr int kDepth = 1;
 constexpr int kFusedDepth = 4;
-constexpr int kFusedTokDepth = 2;  // token-major (matrix-core body: 24 registers per window and lane; 3, 4 slower)
+constexpr int kFusedTokDepth = 2;
 // Share of each fused workgroup's suffix windows that its streaming waves take
 // (in 1/256); the stage-1 waves take the rest after their stage-1 unit.
 constexpr int kFusedSplit = 208;
 static_assert(kFusedSplit >= 128 && kFusedSplit < 256, "ChunkMap::none_empty assumes a share in [1/2, 1)");
 
 // LDS layout (bytes) of the stream body for G query heads per group and NW waves;
-// STASH (the token-major body) adds the merged results of a phase's segments,
-// held until the phase's window loop is done; MF (the matrix-core body) adds
-// each wave's V transpose slot: 8 token rows of 256 bytes at a 288-byte pitch
-// (the pitch puts the 4 rows of a transpose read in distinct bank groups).
+// TOK (the token-major body) adds the merged results of a phase's segments,
+// held until the phase's window loop is done, and each wave's V transpose slot:
+// 8 token rows of 256 bytes at a 288-byte pitch (the pitch puts the 4 rows of a
+// transpose read in distinct bank groups).
 constexpr int kVtPitch = 288;
-template <int G, int NW, bool STASH = false, bool MF = false>
+template <int G, int NW, bool TOK = false>
 struct SfxLds {
     static constexpr int kCw = 0;                                        // int cw[kMaxBatch + 1]
     static constexpr int kLen = ((kMaxBatch + 1) * 4 + 15) / 16 * 16;   // int len[kMaxBatch]
     static constexpr int kWtot = kLen + kMaxBatch * 4;                   // int wtot[NW]
     static constexpr int kTab = kWtot + 64;               // int pair tab[kTable + 8] (8 padding entries)
-    static constexpr int kPw = kTab + (kTable + 8) * 8;  // float pw[NW][8][8] p rows
+    static constexpr int kPw = kTab + (kTable + 8) * 8;  // float pw[NW][8][8] p rows (dims-major)
     static constexpr int kQs = kPw + NW * 8 * 8 * 4;                     // bf16 q[kQSlots][G][kD]
     static constexpr int kX = G <= 4 ? 2 : 1;                            // exchange ring slots
     static constexpr int kXo = kQs + kQSlots * G * kD * 2;               // float xo[kX][NW][G][kD]
     static constexpr int kXml = kXo + kX * NW * G * kD * 4;              // float xml[kX][NW][G][2]
     static constexpr int kXsync = kXml + kX * NW * G * 2 * 4;            // int cnt[kX], gen[kX]
     static constexpr int kBar = kXsync + 2 * kX * 4;                     // int bar[2] (group barrier)
-    static constexpr int kSo = (kBar + 8 + 15) / 16 * 16;                // float so[kQSlots][G][kD] (STASH)
-    static constexpr int kSl = kSo + (STASH ? kQSlots * G * kD * 4 : 0); // float sl[kQSlots][G]
-    static constexpr int kSb = kSl + (STASH ? kQSlots * G * 4 : 0);      // int sb[kQSlots]
-    static constexpr int kVt = (kSb + (STASH ? kQSlots * 4 : 0) + 15) / 16 * 16;  // char vt[NW][8][kVtPitch] (MF)
-    static constexpr int kBytes = kVt + (MF ? NW * 8 * kVtPitch : 0);
+    static constexpr int kSo = (kBar + 8 + 15) / 16 * 16;                // float so[kQSlots][G][kD] (TOK)
+    static constexpr int kSl = kSo + (TOK ? kQSlots * G * kD * 4 : 0);   // float sl[kQSlots][G]
+    static constexpr int kSb = kSl + (TOK ? kQSlots * G * 4 : 0);        // int sb[kQSlots]
+    static constexpr int kVt = (kSb + (TOK ? kQSlots * 4 : 0) + 15) / 16 * 16;  // char vt[NW][8][kVtPitch] (TOK)
+    static constexpr int kBytes = kVt + (TOK ? NW * 8 * kVtPitch : 0);
     static_assert(kTab % 16 == 0 && kPw % 16 == 0 && kQs % 16 == 0 && kXo % 16 == 0 && kXml % 8 == 0 &&
                       kSo % 16 == 0,
                   "aligned LDS rows");
@@ -305,25 +306,12 @@ __device__ __forceinline__ int64_t clamp_len(const SuffixArgs &a, int64_t kvl) {
 // of a grid of a.kv_heads * a.chunks, with the group's LDS at smem and its own
 // barrier. Windows hold 8 NW tokens.
 //
-// Two lane layouts for V and the value accumulators:
-// * TOK = false (dims-major): lane (hf, dd) holds dims 4dd .. 4dd+3 of 4 tokens;
-//   p reaches it through a per-wave LDS row and q is read from LDS per window.
-//   4 accumulators per head: fits 128 registers.
-// * TOK = true (token-major, G <= 4): V uses K's layout, lane (t, c) holds dims
-//   8c .. 8c+7 and 64+8c .. 64+8c+7 of token t, so the lane already owns the p of
-//   its token; q sits in registers for the whole segment. The window loop then
-//   makes no LDS access besides one table read, and its arithmetic never waits
-//   on the LDS pipe (which the fused kernel's stage-1 waves keep busy). 16
-//   accumulators per head, summed over the 8 token slots when a segment closes.
-//   The merged result of a segment waits in an LDS stash, and the role's waves
-//   write a phase's results out together after its window loop: a store in the
-//   loop would count in the same vmcnt as the window loads, so every later wait
-//   of the merging wave would also wait for its acknowledgement (or for loads
-//   issued after it), a stall of about a round trip per merge.
-//
-// MF (with TOK: the same table, segments, exchange ring and stash) computes a
-// window on the matrix cores instead of the vector ALU; a wave still owns 8
-// tokens of every window, and lane (g, n) = (lane / 16, lane % 16):
+// Two bodies:
+// * TOK = false (dims-major, vector ALU): lane (hf, dd) holds dims 4dd .. 4dd+3
+//   of 4 tokens; p reaches it through a per-wave LDS row and q is read from LDS
+//   per window. 4 accumulators per head: fits 128 registers.
+// * TOK = true (token-major on the matrix cores, G <= 4, 4 waves): a wave owns 8
+//   tokens of every window, and lane (g, n) = (lane / 16, lane % 16):
 // * S^T = K q^T on v_mfma_f32_16x16x32_bf16: A = K, row n = token n of the wave's
 //   8 (rows 8-15 read nothing: zeros), dims 32 s + 8 g .. + 7 at step s, straight
 //   from global memory; B = q of head n, the same dims. The result puts token
@@ -338,24 +326,27 @@ __device__ __forceinline__ int64_t clamp_len(const SuffixArgs &a, int64_t kvl) {
 // * The softmax state of head n sits in lane (g, n), the same for every g: the
 //   running max is reduced over the 4 groups when it moves, the row sum when the
 //   segment closes, and O^T needs no reduction (the MFMA summed the tokens).
+// * The merged result of a segment waits in an LDS stash, and the waves write a
+//   phase's results out together after its window loop: a store in the loop
+//   would count in the same vmcnt as the window loads, so every later wait of
+//   the merging wave would also wait for its acknowledgement (or for loads
+//   issued after it), a stall of about a round trip per merge.
 //
 // Two bodies on one CU may share one scan: the body given scan_src (the other
 // body's LDS) skips its own, waits until scan_flag is set and reads the other's
 // lengths and window prefix sums; the body given only scan_flag sets it once its
 // scan is complete.
-template <int G, int NW, int D, bool TOK, bool MF, class Bar>
+template <int G, int NW, int D, bool TOK, class Bar>
 __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS char *smem, int lb, int tid,
                                                    const Bar &bar, CK_LDS int *scan_flag = nullptr,
                                                    const CK_LDS char *scan_src = nullptr) {
-    static_assert(!TOK || G <= 4, "token-major layout: at most 4 query heads per group");
-    static_assert(!MF || (TOK && NW == 4), "the matrix-core body runs on the token-major machinery, 4 waves");
+    static_assert(!TOK || (G <= 4 && NW == 4), "token-major body: at most 4 query heads per group, 4 waves");
     static_assert(D + 1 <= 8, "table padding: D + 1 entries past a phase");
     constexpr int NB = D + 1;  // register ring slots: D windows in flight + the one in use
-    constexpr int kAcc = TOK ? 16 : 4;  // value accumulators per head and lane
     constexpr int kThr = NW * 64;
     constexpr int kWin = 8 * NW;         // tokens per window
     constexpr int kWpp = kPage / kWin;   // windows per page
-    using L = SfxLds<G, NW, TOK, MF>;
+    using L = SfxLds<G, NW, TOK>;
     CK_LDS int *cw = (CK_LDS int *)((scan_src ? scan_src : smem) + L::kCw);
     CK_LDS int *len = (CK_LDS int *)((scan_src ? scan_src : smem) + L::kLen);
     CK_LDS int *wtot = (CK_LDS int *)(smem + L::kWtot);
@@ -463,43 +454,42 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     // ---- per-lane constants ------------------------------------------------------------
     const int64_t tokb = a.tok_stride * 2;                      // bytes between token rows
     const uint32_t koff = (uint32_t)((8 * wid + t) * tokb + c * 16);   // K byte offset in a window
-    const uint32_t voff = TOK ? koff : (uint32_t)((8 * wid + hf) * tokb + dd * 8);  // V byte offset
+    const uint32_t voff = (uint32_t)((8 * wid + hf) * tokb + dd * 8);  // dims-major V byte offset
     const uint32_t win_bytes = (uint32_t)(kWin * tokb);          // a window's buffer range
     const char *kbase = reinterpret_cast<const char *>(a.k) + (int64_t)gk * a.head_off * 2;
     const char *vbase = reinterpret_cast<const char *>(a.v) + (int64_t)gk * a.head_off * 2;
     const int64_t pgb = a.page_stride * 2;
     const uint32_t pg32 = (uint32_t)pgb, win32 = win_bytes, tok32 = (uint32_t)tokb;  // token-major addressing
-    // matrix-core body: lane (mg, mn); its K rows (token 8 wid + mn, 16 bytes at
-    // 64 s + 16 mg for step s; rows 8-15 read nothing), its V bytes in the wave's
-    // LDS slot (written by lane (t, c), read back transposed: tile T at + 32 T) and
-    // the addend of its scores (-inf: a padding row or head)
+    // token-major body: lane (mg, mn); its K rows (token 8 wid + mn, 16 bytes at
+    // 64 s + 16 mg for step s; rows 8-15 read nothing), its V bytes (lane (t, c):
+    // token t, bytes 16 c and 128 + 16 c, at koff) in the wave's LDS slot, read
+    // back transposed (tile T at + 32 T), and the addend of its scores (-inf: a
+    // padding row or head)
     const int mn = lane & 15, mg = lane >> 4;
-    const uint32_t kmoff = mn < 8 ? (uint32_t)((8 * wid + mn) * tokb + 16 * mg) : kOob;
+    const uint32_t kfoff = mn < 8 ? (uint32_t)((8 * wid + mn) * tokb + 16 * mg) : kOob;
     CK_LDS char *vt = smem + L::kVt + wid * 8 * kVtPitch;
     const int vwo = t * kVtPitch + 16 * c;
     const int vro = (4 * (mg & 1) + (mn >> 2)) * kVtPitch + 8 * (mn & 3);
     const float sbias = (mg < 2 && mn < G) ? 0.f : -INFINITY;
 
-    float m[G], l[G], acc[G][kAcc];
-    // token-major: m + kTau (the rescale trigger) and the exponent offset (m, 0
-    // while m = -inf), kept beside m: they change only when m does
-    float mt[G], mz[G];
-    // matrix-core body: the O^T tiles (dims 16 T + 4 mg + r of head mn), head mn's
-    // softmax state (m, m + kTau, the exponent offset, this lane's share of the
-    // row sum), q fragments, and the P^T operand (hi, lo) of the pending window
+    float m[G], l[G], acc[G][4];  // dims-major: per head, 4 value accumulators
+    // token-major: the O^T tiles (dims 16 T + 4 mg + r of head mn), head mn's
+    // softmax state (m; m + kTau, the rescale trigger; the exponent offset, m or
+    // 0 while m = -inf; this lane's share of the row sum), q fragments, and the
+    // P^T operand (hi, lo) of the pending window
     f32x4 oacc[8];
     float m1, mt1, mz1, l1;
     u32x4 qf[4];
     uint32_t ph[2], pl[2];
     int nclose = 0;  // segments closed so far (exchange ring position)
     int qslot = 0;   // segment of the current phase
-    u32x4 kbuf[NB][MF ? 4 : 2];
+    u32x4 kbuf[NB][TOK ? 4 : 2];
     using VSlot = std::conditional_t<TOK, u32x4[2], u32x2[4]>;
     VSlot vbuf[NB];
-    // q in registers from the window that opens a segment: the token-major body,
-    // and the stand-alone dims-major body above 4 heads (one workgroup per CU, so
-    // the 8 G registers cost no occupancy); else q is read from LDS per window
-    constexpr bool kQReg = TOK || (G > 4 && NW == kWaves);
+    // dims-major: q in registers from the window that opens a segment in the
+    // stand-alone body above 4 heads (one workgroup per CU, so the 8 G registers
+    // cost no occupancy); else q is read from LDS per window
+    constexpr bool kQReg = G > 4 && NW == kWaves;
     u32x4 qr[kQReg ? G : 1][2];  // this lane's 16 q dims of each head
     int eyr[NB];               // packed table fields of the window in each ring slot
     constexpr int kPwRow = (G + 3) / 4 * 4;  // floats per token in this wave's p rows
@@ -534,10 +524,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(vbase + w.off), (short)0, w.range, kRsrcFlags);
         k0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)koff, 0, 0));
         k1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)(koff + 128), 0, 0));
-        if constexpr (TOK) {
-            vv[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, (int)koff, 0, 0));
-            vv[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, (int)(koff + 128), 0, 0));
-        } else {
+        if constexpr (!TOK) {  // the dims-major body's loads
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 vv[j] = __builtin_bit_cast(
@@ -545,13 +532,13 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         }
     };
 
-    // matrix-core body: a window's K rows as the 4 A fragments of its score MFMAs
-    auto issue_kmf = [&](const TokWin &w, u32x4 *kf) __attribute__((always_inline)) {
+    // token-major: a window's K rows as the 4 A fragments of its score MFMAs
+    auto issue_kfrag = [&](const TokWin &w, u32x4 *kf) __attribute__((always_inline)) {
         const __amdgpu_buffer_rsrc_t r =
             __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(kbase + w.off), (short)0, w.range, kRsrcFlags);
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4)
-            kf[s4] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(kmoff + 64 * s4), 0, 0));
+            kf[s4] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(kfoff + 64 * s4), 0, 0));
     };
 
     // Token-major windows issue their K and V halves at different points of a step
@@ -641,71 +628,33 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
 
     // Token-major: the state of a new segment, set at the start and by every close
     // (a segment opens at the chunk's first window or right after the previous
-    // segment's close); the close's reduction then works on registers it owns.
+    // segment's close).
     auto reset_seg = [&]() __attribute__((always_inline)) {
-        if constexpr (MF) {
-            m1 = -INFINITY;
-            mt1 = -INFINITY;
-            mz1 = 0.f;
-            l1 = 0.f;
+        m1 = -INFINITY;
+        mt1 = -INFINITY;
+        mz1 = 0.f;
+        l1 = 0.f;
 #pragma unroll
-            for (int T = 0; T < 8; ++T) oacc[T] = f32x4{0.f, 0.f, 0.f, 0.f};
-            return;
-        }
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            m[h] = -INFINITY;
-            mt[h] = -INFINITY;
-            mz[h] = 0.f;
-            l[h] = 0.f;
-#pragma unroll
-            for (int e = 0; e < kAcc; ++e) acc[h][e] = 0.f;
-        }
+        for (int T = 0; T < 8; ++T) oacc[T] = f32x4{0.f, 0.f, 0.f, 0.f};
     };
 
     // Closes segment b (sequence b's windows in this range): folds the lanes' partial
     // sums, hands the wave's (O, m, l) to the exchange ring, and the last wave in
     // merges the NW partials and writes the result (TOK: into the phase's stash).
     auto close_seg = [&](int b) __attribute__((always_inline)) {
-        // token-major with 4 heads: a reduce-scatter over the 8 token slots. The
-        // 64 accumulators of a lane, flat index f = 16 h + e, are halved twice by
-        // lane swaps (the half-wave bit keeps f's bit 5, the 16-lane-row bit f's
-        // bit 4) and the last slot bit is summed by DPP: lane (s5, s4, s3, c) ends
-        // with head 2 s5 + s4, all 16 of its dims, in 112 instructions instead of
-        // 320 for summing every accumulator over all 8 slots.
-        float f2[16];
-        float lt1 = 0.f;  // matrix-core body: head mn's row sum over the 4 groups
-        if constexpr (MF) {
+        // token-major: head mn's row sum over the 4 groups; O^T needs no reduction
+        // (the MFMAs summed over the tokens). Dims-major: each head's row sum over
+        // the 8 token slots, its accumulators over the two half-waves.
+        float lt1 = 0.f;
+        if constexpr (TOK) {
             lt1 = sum_xor32(sum_xor16(l1));
         } else {
 #pragma unroll
             for (int h = 0; h < G; ++h) l[h] = sum_slots(l[h]);
-        }
-        if constexpr (MF) {
-            // O^T needs no reduction: the MFMAs summed over the tokens
-        } else if constexpr (TOK && G == 4) {
-            float f1[32];
-#pragma unroll
-            for (int j = 0; j < 32; ++j) {
-                const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[j >> 4][j & 15]),
-                                                                __float_as_uint(acc[(j + 32) >> 4][j & 15]), false,
-                                                                false);
-                f1[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-            }
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const auto r =
-                    __builtin_amdgcn_permlane16_swap(__float_as_uint(f1[j]), __float_as_uint(f1[j + 16]), false, false);
-                f2[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-            }
-#pragma unroll
-            for (int e = 0; e < 16; ++e) f2[e] += CK_DPP(f2[e], 0x128);  // row_ror:8: lane ^ 8
-        } else {
 #pragma unroll
             for (int h = 0; h < G; ++h) {
 #pragma unroll
-                for (int e = 0; e < kAcc; ++e)  // dims-major: the two half-waves; token-major: the 8 token slots
-                    acc[h][e] = TOK ? sum_slots(acc[h][e]) : sum_xor32(acc[h][e]);
+                for (int e = 0; e < 4; ++e) acc[h][e] = sum_xor32(acc[h][e]);
             }
         }
         const int r = nclose % R;
@@ -721,7 +670,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         }
         CK_LDS float *xo_r = xo + r * NW * G * kD;
         CK_LDS float *xml_r = xml + r * NW * G * 2;
-        if constexpr (MF) {
+        if constexpr (TOK) {
             if (mn < G) {
 #pragma unroll
                 for (int T = 0; T < 8; ++T)
@@ -731,35 +680,13 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                     xml_r[(wid * G + mn) * 2 + 1] = lt1;
                 }
             }
-        } else if constexpr (TOK && G == 4) {
-            if ((lane & 8) == 0) {
-                CK_LDS float *dst = xo_r + (wid * G + (lane >> 4)) * kD + 8 * c;
-                *reinterpret_cast<CK_LDS f32x4 *>(dst) = f32x4{f2[0], f2[1], f2[2], f2[3]};
-                *reinterpret_cast<CK_LDS f32x4 *>(dst + 4) = f32x4{f2[4], f2[5], f2[6], f2[7]};
-                *reinterpret_cast<CK_LDS f32x4 *>(dst + 64) = f32x4{f2[8], f2[9], f2[10], f2[11]};
-                *reinterpret_cast<CK_LDS f32x4 *>(dst + 68) = f32x4{f2[12], f2[13], f2[14], f2[15]};
-            }
-        } else if constexpr (TOK) {
-            // every token slot holds the sums: slot h writes head h
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                if (t == h) {
-                    CK_LDS float *dst = xo_r + (wid * G + h) * kD + 8 * c;
-                    *reinterpret_cast<CK_LDS f32x4 *>(dst) = f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
-                    *reinterpret_cast<CK_LDS f32x4 *>(dst + 4) = f32x4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
-                    *reinterpret_cast<CK_LDS f32x4 *>(dst + 64) =
-                        f32x4{acc[h][8], acc[h][9], acc[h][10], acc[h][11]};
-                    *reinterpret_cast<CK_LDS f32x4 *>(dst + 68) =
-                        f32x4{acc[h][12], acc[h][13], acc[h][14], acc[h][15]};
-                }
-            }
         } else if (hf == 0) {
 #pragma unroll
             for (int h = 0; h < G; ++h)
                 *reinterpret_cast<CK_LDS f32x4 *>(xo_r + (wid * G + h) * kD + 4 * dd) =
                     f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
         }
-        if (!MF && lane == 0) {
+        if (!TOK && lane == 0) {
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 xml_r[(wid * G + h) * 2] = m[h];
@@ -895,110 +822,14 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
       }
     };
 
-    // Token-major window step, pipelined by one window: step n issues the K rows of
-    // window n + D, computes the scores of window n and the values of window n - 1
-    // (its p kept from the step before, its V rows still in their ring slot) -- two
-    // independent chains in one basic block, so each fills the other's latencies --
-    // then issues window n + D's V rows into the slot window n - 1's values just
-    // left, closes window n - 1's segment if it ends there and finishes window n's
-    // softmax. The table entry of the window to issue was read one step ahead and
-    // the packed fields of each window travel in the ring with its data, so the
-    // step's only LDS access is off its critical path.
-    float pp[G];     // p of window n - 1 (0 before a phase's first window)
-    int eypend = 0;  // packed table fields of window n - 1
-    auto pv_tok = [&](const float *p, const VSlot &vv) __attribute__((always_inline)) {
-        if constexpr (TOK) {
-            const u32x4 v0 = vv[0], v1 = vv[1];
-            float vf[16];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                vf[2 * i] = bf16_lo(v0[i]);
-                vf[2 * i + 1] = bf16_hi(v0[i]);
-                vf[8 + 2 * i] = bf16_lo(v1[i]);
-                vf[9 + 2 * i] = bf16_hi(v1[i]);
-            }
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) acc[h][e] = fmaf(p[h], vf[e], acc[h][e]);
-            }
-        }
-    };
-    auto step_tok = [&](auto jc, int n, int np) __attribute__((always_inline)) {
-      if constexpr (TOK) {
-        constexpr int J = decltype(jc)::value;
-        constexpr int JI = (J + D) % NB;  // window n + D, into the slot of window n - 1
-        const i32x2 ei = enext;
-        const TokWin wi = tok_win(ei);
-        issue_half(kbase, wi, kbuf[JI][0], kbuf[JI][1]);
-        const int ey = eyr[J];
-        const int eyp = eypend;
-        eyr[JI] = __builtin_amdgcn_readfirstlane(ei[1]);
-        if (tab_first(ey)) {
-            // window n opens a segment: its q rows sit in the slot after the one of
-            // the segment window n - 1 may still close
-            const CK_LDS char *qrow = qs + (qslot + (tab_last(eyp) ? 1 : 0)) * G * (kD * 2) + c * 16;
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                qr[h][0] = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2));
-                qr[h][1] = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2) + 128);
-            }
-        }
-        // the table entry for the next step, read after the q rows: the score
-        // chains wait for the q rows by the LDS counter, and an earlier read would
-        // be waited for with them
-        enext = tab[n + D + 1];  // at most np + D: a padding entry past the phase
-        float s[G];  // scores of window n, then its p
-        {
-            const u32x4 k0 = kbuf[J][0], k1 = kbuf[J][1];
-#pragma unroll
-            for (int h = 0; h < G; ++h) s[h] = sum8(dot16(k0, k1, qr[h][0], qr[h][1])) * a.scale_log2;
-        }
-        pv_tok(pp, vbuf[JI]);
-        if constexpr (TOK) issue_half(vbase, wi, vbuf[JI][0], vbuf[JI][1]);
-        if (tab_last(eyp)) close_seg(tab_b(eyp));
-        eypend = ey;
-        {
-            // tokens past the sequence's end (their K rows read as 0; all 8 when t1 = 0)
-            const int t1 = min(max(tab_tv(ey) - 8 * wid, 0), 8);
-            if (t1 < 8) {
-                asm volatile("");  // a branch (a sequence's last window), not 8 selects per window
-#pragma unroll
-                for (int h = 0; h < G; ++h) s[h] = t < t1 ? s[h] : -INFINITY;
-            }
-        }
-        bool trig = false;
-#pragma unroll
-        for (int h = 0; h < G; ++h) trig |= s[h] > mt[h];  // m = -inf: always
-        if (__builtin_amdgcn_ballot_w64(trig)) {
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const float m_new = fmaxf(m[h], max_slots(s[h]));
-                if (m_new > m[h]) {
-                    const float f = exp2_fast(m[h] - m_new);  // 0 from -inf
-#pragma unroll
-                    for (int e = 0; e < kAcc; ++e) acc[h][e] *= f;
-                    l[h] *= f;
-                    m[h] = m_new;
-                    mt[h] = m_new + kTau;
-                    mz[h] = m_new;
-                }
-            }
-        }
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            pp[h] = exp2_fast(s[h] - mz[h]);  // 0 for masked tokens
-            l[h] += pp[h];
-        }
-      }
-    };
-    // Matrix-core values of the pending window: its V rows (lane (t, c) holds 32
+    int eypend = 0;  // packed table fields of window n - 1 (token-major)
+    // Token-major values of the pending window: its V rows (lane (t, c) holds 32
     // bytes of token t) into the wave's LDS slot, back as the V^T fragments of the 8
     // dim tiles, then O^T += V^T P^T for the hi and the lo term of P. The slot is
     // written and read by this wave only, whose LDS operations run in issue order.
     typedef short s16x4 __attribute__((ext_vector_type(4)));
-    auto pv_mf = [&](const VSlot &vv) __attribute__((always_inline)) {
-      if constexpr (MF) {
+    auto pv_tok = [&](const VSlot &vv) __attribute__((always_inline)) {
+      if constexpr (TOK) {
         *reinterpret_cast<CK_LDS u32x4 *>(vt + vwo) = vv[0];
         *reinterpret_cast<CK_LDS u32x4 *>(vt + vwo + 128) = vv[1];
         uint2 vtf[8];
@@ -1014,18 +845,21 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         }
       }
     };
-    // Matrix-core window step, pipelined like the token-major one: step n issues
-    // window n + D's K rows, computes window n's scores, then window n - 1's values
-    // (its P kept from the step before, its V rows still in their ring slot),
-    // issues window n + D's V rows into that slot, closes window n - 1's segment if
-    // it ends there and finishes window n's softmax.
-    auto step_mf = [&](auto jc, int n, int np) __attribute__((always_inline)) {
-      if constexpr (MF) {
+    // Token-major window step, pipelined by one window: step n issues the K rows of
+    // window n + D, computes the scores of window n and the values of window n - 1
+    // (its P kept from the step before, its V rows still in their ring slot) -- two
+    // independent chains in one basic block, so each fills the other's latencies --
+    // then issues window n + D's V rows into the slot window n - 1's values just
+    // left, closes window n - 1's segment if it ends there and finishes window n's
+    // softmax. The table entry of the window to issue was read one step ahead and
+    // the packed fields of each window travel in the ring with its data.
+    auto step_tok = [&](auto jc, int n, int np) __attribute__((always_inline)) {
+      if constexpr (TOK) {
         constexpr int J = decltype(jc)::value;
         constexpr int JI = (J + D) % NB;  // window n + D, into the slot of window n - 1
         const i32x2 ei = enext;
         const TokWin wi = tok_win(ei);
-        issue_kmf(wi, kbuf[JI]);
+        issue_kfrag(wi, kbuf[JI]);
         const int ey = eyr[J];
         const int eyp = eypend;
         eyr[JI] = __builtin_amdgcn_readfirstlane(ei[1]);
@@ -1044,7 +878,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         for (int s4 = 0; s4 < 4; ++s4)
             sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kbuf[J][s4]),
                                                          __builtin_bit_cast(bf16x8, qf[s4]), sc, 0, 0, 0);
-        pv_mf(vbuf[JI]);
+        pv_tok(vbuf[JI]);
         issue_half(vbase, wi, vbuf[JI][0], vbuf[JI][1]);
         if (tab_last(eyp)) close_seg(tab_b(eyp));
         eypend = ey;
@@ -1100,10 +934,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
       if constexpr (TOK) {
         const int js = (np - 1) % NB;  // wave-uniform
         static_for<NB>([&](auto jc) __attribute__((always_inline)) {
-            if (js == decltype(jc)::value) {
-                if constexpr (MF) pv_mf(vbuf[decltype(jc)::value]);
-                else pv_tok(pp, vbuf[decltype(jc)::value]);
-            }
+            if (js == decltype(jc)::value) pv_tok(vbuf[decltype(jc)::value]);
         });
         if (tab_last(eypend)) close_seg(tab_b(eypend));
       }
@@ -1182,8 +1013,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             if constexpr (TOK) {
                 const i32x2 e = tab[j];  // j < D: a padding entry when j >= np
                 const TokWin w = tok_win(e);
-                if constexpr (MF) issue_kmf(w, kbuf[j]);
-                else issue_half(kbase, w, kbuf[j][0], kbuf[j][1]);
+                issue_kfrag(w, kbuf[j]);
                 issue_half(vbase, w, vbuf[j][0], vbuf[j][1]);
                 eyr[j] = __builtin_amdgcn_readfirstlane(e[1]);
             } else {
@@ -1197,8 +1027,6 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             enext = tab[D];
             // "window -1" of the pipelined step (slot NB - 1): no values, no close;
             // its V slot is zeroed so that p = 0 times it stays 0
-#pragma unroll
-            for (int h = 0; h < G; ++h) pp[h] = 0.f;
             ph[0] = ph[1] = pl[0] = pl[1] = 0u;
             vbuf[NB - 1][0] = u32x4{0u, 0u, 0u, 0u};
             vbuf[NB - 1][1] = u32x4{0u, 0u, 0u, 0u};
@@ -1210,8 +1038,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         int n = 0;
         for (int it = np / NB; it > 0; --it) {
             static_for<NB>([&](auto jc) __attribute__((always_inline)) {
-                if constexpr (MF) step_mf(jc, n + decltype(jc)::value, np);
-                else if constexpr (TOK) step_tok(jc, n + decltype(jc)::value, np);
+                if constexpr (TOK) step_tok(jc, n + decltype(jc)::value, np);
                 else step(jc, n + decltype(jc)::value, np);
             });
             n += NB;
@@ -1219,8 +1046,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
         const int rem = np - n;
         static_for<NB>([&](auto jc) __attribute__((always_inline)) {
             if (decltype(jc)::value < rem) {
-                if constexpr (MF) step_mf(jc, n + decltype(jc)::value, np);
-                else if constexpr (TOK) step_tok(jc, n + decltype(jc)::value, np);
+                if constexpr (TOK) step_tok(jc, n + decltype(jc)::value, np);
                 else step(jc, n + decltype(jc)::value, np);
             }
         });
@@ -1241,30 +1067,23 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     }
 }
 
-// Up to 4 query heads per group the body fits in 128 registers: 4 waves per
-// SIMD, two workgroups per CU. Above, its per-head state needs more, and the
-// grid's second half runs as the first half's workgroups finish.
+// Up to 4 query heads per group: the token-major body on the matrix cores (the
+// fused kernel's streaming body) on 4 waves, two workgroups per CU (64 KB of LDS
+// and at most 256 registers each).
 template <int G>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void suffix_stream_kernel(SuffixArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void suffix_stream_kernel(SuffixArgs a) {
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-    suffix_stream_body<G, kWaves, kDepth, false, false>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
+    suffix_stream_body<G, 4, kFusedTokDepth, true>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
 }
+static_assert(SfxLds<4, 4, true>::kBytes <= 80 * 1024, "two token-major stream workgroups per CU");
+// Above 4 query heads per group: the dims-major body on 8 waves; its per-head
+// state needs more registers, and the grid's second half runs as the first
+// half's workgroups finish.
 template <int G>
 __global__ __launch_bounds__(kThreads) void suffix_stream_wide_kernel(SuffixArgs a) {
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-    suffix_stream_body<G, kWaves, kDepth, false, false>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
+    suffix_stream_body<G, kWaves, kDepth, false>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
 }
-// Up to 4 query heads per group on the matrix cores: the fused kernel's streaming
-// body on 4 waves, two workgroups per CU (its LDS: 64 KB each).
-template <int G>
-constexpr bool kSuffixMf = G <= 4;
-template <int G>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void suffix_stream_mf_kernel(SuffixArgs a) {
-    extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-    suffix_stream_body<G, 4, kFusedTokDepth, true, true>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x,
-                                                         WgBarrier{});
-}
-static_assert(SfxLds<4, 4, true, true>::kBytes <= 80 * 1024, "two matrix-core stream workgroups per CU");
 
 // Folds the partials of one query head of a sequence cut by chunk boundaries
 // (chunks ca < cb): the tail slot (1) of chunk ca and the head slot (0) of every
@@ -1509,11 +1328,8 @@ __global__ __launch_bounds__(kMaxGroup * 32) void cascade_epilogue_kernel(Epilog
 // waves finish. Each role has its own LDS region and barrier; neither waits
 // for the other.
 constexpr int kFusedS1Lds = s1::wide_lds_bytes<3>();
-// the stream body on 4 waves: token-major windows on the matrix cores up to 4 heads
 template <int G>
-constexpr bool kFusedMf = G <= 4;
-template <int G>
-using FusedSfx = SfxLds<G, 4, (G <= 4), kFusedMf<G>>;
+using FusedSfx = SfxLds<G, 4, (G <= 4)>;  // the stream body's layout on 4 waves (token-major up to 4 heads)
 template <int G>
 constexpr int fused_lds_bytes() { return kFusedS1Lds + FusedSfx<G>::kBytes + 32; }
 static_assert(fused_lds_bytes<4>() <= 160 * 1024 && fused_lds_bytes<kMaxGroup>() <= 160 * 1024,
@@ -1551,7 +1367,7 @@ __global__ __launch_bounds__(512) void cascade_fused_kernel(s1::Stage1Args s1a, 
         constexpr int kRoleRot = 3;
         const int g = ((int)blockIdx.x + kRoleRot) % sa.kv_heads, j = (int)blockIdx.x / sa.kv_heads;
         // the streaming waves scan the lengths; the stage-1 waves reuse that scan
-        suffix_stream_body<G, 4, (G <= 4 ? kFusedTokDepth : kFusedDepth), (G <= 4), kFusedMf<G>>(
+        suffix_stream_body<G, 4, (G <= 4 ? kFusedTokDepth : kFusedDepth), (G <= 4)>(
             sa, smem + (role ? 0 : kFusedS1Lds), (2 * j + role) * sa.kv_heads + g, threadIdx.x & 255, bar, bars + 4,
             role ? smem + kFusedS1Lds : nullptr);
     }
@@ -1582,19 +1398,14 @@ int launch_fused(const s1::Stage1Args &s1a, int64_t n1, const SuffixArgs &a, con
 template <int G>
 int launch_suffix(const SuffixArgs &a, bool fixup, const EpilogueArgs *epi, hipStream_t st) {
     static std::atomic<uint64_t> lds_set{0};
-    constexpr int kLds = kSuffixMf<G> ? SfxLds<G, 4, true, true>::kBytes : SfxLds<G, kWaves>::kBytes;
+    constexpr int kLds = G <= 4 ? SfxLds<G, 4, true>::kBytes : SfxLds<G, kWaves>::kBytes;
     const void *fn;
-    if constexpr (kSuffixMf<G>) fn = reinterpret_cast<const void *>(&suffix_stream_mf_kernel<G>);
-    else if constexpr (G <= 4) fn = reinterpret_cast<const void *>(&suffix_stream_kernel<G>);
+    if constexpr (G <= 4) fn = reinterpret_cast<const void *>(&suffix_stream_kernel<G>);
     else fn = reinterpret_cast<const void *>(&suffix_stream_wide_kernel<G>);
     int rc = ensure_dynamic_lds(fn, kLds, lds_set);
     if (rc != CK_OK) return rc;
-    if constexpr (kSuffixMf<G>)
-        hipLaunchKernelGGL(suffix_stream_mf_kernel<G>, dim3((unsigned)(a.kv_heads * a.chunks)), dim3(256), kLds, st,
-                           a);
-    else if constexpr (G <= 4)
-        hipLaunchKernelGGL(suffix_stream_kernel<G>, dim3((unsigned)(a.kv_heads * a.chunks)), dim3(kThreads), kLds,
-                           st, a);
+    if constexpr (G <= 4)
+        hipLaunchKernelGGL(suffix_stream_kernel<G>, dim3((unsigned)(a.kv_heads * a.chunks)), dim3(256), kLds, st, a);
     else
         hipLaunchKernelGGL(suffix_stream_wide_kernel<G>, dim3((unsigned)(a.kv_heads * a.chunks)), dim3(kThreads),
                            kLds, st, a);
