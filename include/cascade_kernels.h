@@ -131,7 +131,7 @@ int ck_fa_fp32_stage1(const void *q, const void *k, const void *v, const int32_t
 
 /* ============================================================================
  * Per-sequence paged decode attention over each sequence's own suffix
- * (one query token per sequence, GQA, no MFMA).
+ * (one query token per sequence, GQA; P at fp32 precision).
  *   q            bf16 [batch, num_heads, 128]
  *   k, v         bf16 paged pool in layout kv_layout: CK_KV_NHD
  *                [num_blocks, 128, kv_heads, 128] or CK_KV_BNSD

@@ -1,7 +1,8 @@
 """GPU parity of suffix_decode (stage 2) and of the full cascade (stage 1 + suffix
 + merge) against the oracle and dense attention over the concatenated KV.
 
-suffix_decode keeps P in fp32, so its oracle is the unquantised online softmax.
+suffix_decode keeps P at fp32 precision (on the matrix cores as two bf16 terms whose sum is P within
+2^-16 P), so its oracle is the unquantised online softmax.
 Its O is bf16: the tolerance is the north-star 2e-3 plus half a bf16 ulp of |O|.
 """
 import numpy as np
