@@ -1,6 +1,7 @@
 // suffix_decode.hip - per-sequence paged decode attention over each sequence's
-// own suffix pages (cascade stage 2) on gfx950: the stand-alone op on the
-// vector ALU, the fused cascade's streaming waves on the matrix cores.
+// own suffix pages (cascade stage 2) on gfx950: the stand-alone op and the
+// fused cascade's streaming waves compute their windows on the matrix cores
+// (the fused kernel above 4 query heads per group on the vector ALU).
 //
 // Role: replaces the closed CANN op npu_fused_infer_attention_score_v2 the
 // reference calls for stage 2 (ascend-kernel/README.md:186-197): one query
@@ -9,70 +10,59 @@
 // yields O = 0, LSE = -inf, which the merge treats as weight 0.
 //
 // Arithmetic: S = q k^T * scale in fp32, online softmax in the log2 domain,
-// fp32 P and fp32 accumulation (no bf16 rounding of P; the matrix-core body
-// feeds P as two bf16 terms whose sum is P within 2^-16), O = acc / l,
-// LSE = ln(l) + max.
+// P at fp32 precision (the matrix-core body feeds P as two bf16 terms whose
+// sum is P within 2^-16) and fp32 accumulation, O = acc / l, LSE = ln(l) + max.
 //
-// MI355X design: HBM-bound streaming with a persistent, balanced grid, and as
-// little vector-ALU work per byte as the arithmetic allows (a wave64 vector
-// instruction occupies its SIMD for 4 cycles; at 8 TB/s a CU receives about
-// 15 bytes per cycle, so every instruction per K/V byte counts).
+// MI355X design: HBM-bound streaming with a persistent, balanced grid and few
+// instructions per byte (at 8 TB/s a CU receives about 15 bytes per cycle; a
+// vector-ALU body of ~190 instructions per 32-token window was bound by its
+// own issue, the matrix-core body takes ~90).
 // * Suffix lengths vary widely (geometric in the benchmark), so the work is cut
-//   into windows of 8 tokens per streaming wave (64 tokens for the 8-wave
-//   kernel) of one sequence (the last window of a sequence may be short), and
-//   workgroup (kv head group g, chunk c) takes the c-th 1/P of the list of all
-//   windows, crossing sequence boundaries: every workgroup streams the same
-//   number of windows and starts once. Two workgroups per CU.
+//   into windows of 8 tokens per streaming wave (32 tokens on 4 waves) of one
+//   sequence (the last window of a sequence may be short), and workgroup (kv
+//   head group g, chunk c) takes the c-th 1/P of the list of all windows,
+//   crossing sequence boundaries: every workgroup streams the same number of
+//   windows and starts once.
 // * Start-up: lengths -> window prefix sums (block scan in LDS), then a table
-//   of the workgroup's windows (page id, first token, valid tokens, sequence,
-//   segment start/end) built in parallel in one round trip that also copies
-//   the first q rows into LDS. The streaming loop reads the table from LDS; no
-//   load in the loop depends on another load.
+//   of the workgroup's windows (page id, valid tokens, sequence, segment
+//   start/end) built in parallel in one round trip that also copies the first
+//   q rows into LDS. The streaming loop reads the table from LDS; no load in
+//   the loop depends on another load.
 // * Two paged K/V layouts: NHD [blocks, 128, kv_heads, 128] (the stage-1 pool)
 //   and BNSD [blocks, kv_heads, 128, 128] (the layout the reference's stage-2
 //   op reads, ascend-kernel/README.md:182-183), so a BNSD pool needs no
 //   transposing copy. A page, a token and a kv head are three strides.
-// * K and V go straight from HBM into registers by buffer loads: no LDS
-//   staging and no barrier in the streaming loop. Each window gets a buffer
-//   descriptor (its first row as base, its 64 rows as range) built with scalar
-//   instructions, so a lane's address is a fixed offset; lanes whose tokens lie
-//   past the sequence's end use an out-of-range offset, which returns zeros and
-//   moves no bytes, and an invalid page id gets an empty range: its rows read
-//   as zeros, the semantics of the pool's unmapped pages.
-// * Each wave owns 8 tokens of every window. For K, lane (t, c) holds token t
-//   and dims 8c .. 8c+7 and 64+8c .. 64+8c+7 (two 16-byte loads); for V, lane
-//   (hf, d) holds dims 4d .. 4d+3 of tokens hf, 2 + hf, 4 + hf, 6 + hf (four
-//   8-byte loads), so the value accumulators are only 4 per query head. A wave
-//   issues the loads of its next window before computing the current one (a
-//   two-slot register ring), so the memory pipe never waits on arithmetic or
-//   on another wave.
-// * Scores: 8 packed bf16 dot products (v_dot2_f32_bf16) and a 3-step DPP sum
-//   over the 8 lanes of a token. The running max is uniform over the wave and
-//   moves only when a score exceeds it by more than 2^kTau (a wave-uniform
-//   branch), so rescaling is rare; any reference point gives the same O and LSE.
-// * Values: p of the wave's 8 tokens goes through a 32-float LDS row per wave
-//   (one write, four broadcast reads), then 4 FMAs per token and head.
-// * Closing a sequence never stops the stream: each wave folds its two
-//   half-waves with one lane swap per accumulator, writes its partial (O, m, l)
-//   into the segment's slot of an LDS exchange ring and counts itself in with an
-//   LDS atomic; the last of the 8 waves merges the 8 partials and writes the
-//   result while the others go on. A wave waits for a ring slot only if it runs
-//   a whole ring ahead of the slowest wave, which itself never waits, so every
-//   wait ends. (The fused kernel's token-major body splits each merge over its
-//   4 waves instead, once all partials are in: one wave doing the whole merge
-//   fell behind the others by it at every close, and the workgroup waits for
-//   its slowest wave.)
+// * K and V go straight from HBM into registers by buffer loads, no barrier in
+//   the streaming loop. Each window gets a buffer descriptor (its first row as
+//   base, its valid rows as range) built with scalar instructions, so a lane's
+//   address is a fixed offset; rows past the sequence's end fall outside the
+//   range (zeros, no bytes moved), and an invalid page id gets an empty range:
+//   its rows read as zeros, the semantics of the pool's unmapped pages.
+// * Token-major body (the stand-alone kernel, the fused kernel up to 4 heads):
+//   scores S^T = K q^T and values O^T += V^T P^T on 16x16 bf16 MFMAs, V^T
+//   through a per-wave LDS slot read back transposed (suffix_stream_body gives
+//   the lane layouts). Dims-major body (the fused kernel above 4 heads): 8
+//   packed bf16 dot products and a DPP sum per score, p through a per-wave LDS
+//   row, 4 value FMAs per token and head. Either way the running max moves only
+//   when a score exceeds it by more than 2^kTau (a wave-uniform branch), so
+//   rescaling is rare; any reference point gives the same O and LSE.
+// * Closing a sequence never stops the stream: each wave writes its partial
+//   (O, m, l) into the segment's slot of an LDS exchange ring and counts itself
+//   in with an LDS atomic. Token-major: once all partials are in, each wave
+//   merges its share into an LDS stash (one wave doing the whole merge fell
+//   behind the others by it at every close), written out after the phase's
+//   loop. Dims-major: the last wave in merges and writes the result while the
+//   others go on. A wave waits for a ring slot only if it runs a whole ring
+//   ahead of the slowest wave, which itself never waits, so every wait ends.
 // * Cascade (stage 1 + suffix + merge): one fused kernel, one workgroup per CU.
 //   Waves 0-3 run the stage-1 body (MFMA, LDS tiles: matrix cores and LDS),
-//   waves 4-7 stream suffix windows (memory pipe; their 4-head groups on the
-//   matrix cores, with one LDS round trip per window to transpose V); each role
-//   synchronises only its own four waves through an LDS counter barrier, so
-//   the two run side by side instead of one kernel after the other, and a
-//   small epilogue kernel merges the two results.
+//   waves 4-7 stream suffix windows; each role synchronises only its own four
+//   waves through an LDS counter barrier, so the two run side by side instead
+//   of one kernel after the other, and a small epilogue kernel merges the two
+//   results.
 // * The range is processed in phases of at most 512 windows and 8 segments.
 //   A phase starts with one round trip that fills the window table and copies
-//   the q rows of its segments into LDS (read per window, which costs far less
-//   LDS bandwidth than the registers it frees); the phase's loop has no barrier.
+//   the q rows of its segments into LDS; the phase's loop has no barrier.
 // * A segment that is a whole sequence writes bf16 O and the LSE directly; a
 //   sequence cut by a chunk boundary leaves fp32 partials that a small fix-up
 //   kernel folds (it also writes O = 0, LSE = -inf for empty suffixes).
@@ -104,8 +94,6 @@ __device__ __forceinline__ void static_for(F &&f) {
 
 constexpr int kD = 128;
 constexpr int kPage = 128;
-constexpr int kWaves = 8;           // waves of the stand-alone stream kernel
-constexpr int kThreads = kWaves * 64;
 constexpr int kMaxGroup = 8;
 constexpr int kMaxBatch = 1024;     // sequences per launch (prefix sums in LDS)
 constexpr int kQSlots = 8;          // segments per phase (their q rows in LDS)
@@ -114,14 +102,11 @@ constexpr float kTau = 8.0f;        // log2 headroom before the running max move
 constexpr uint32_t kOob = 0x80000000u;  // a buffer offset past every window's range
 constexpr int kRsrcFlags = 0x00020000;  // buffer descriptor word 3 for gfx9 raw loads
 
-// windows of loads in flight per wave: dims-major, one in the stand-alone wide
-// kernel (deeper rings of 2-10 windows measured slower in its 16-wave-per-CU
-// form) and 4 in the fused cascade kernel, whose 4 streaming waves per CU carry
-// the CU's whole share; token-major, 2 (24 registers per window and lane; 3 and
-// 4 measured slower in the fused kernel).
-constexpr int kDepth = 1;
+// windows of loads in flight per streaming wave: token-major, 2 (24 registers
+// per window and lane; 3 and 4 measured slower in the fused kernel); dims-major
+// (the fused kernel above 4 heads), 4.
+constexpr int kTokDepth = 2;
 constexpr int kFusedDepth = 4;
-constexpr int kFusedTokDepth = 2;
 // Share of each fused workgroup's suffix windows that its streaming waves take
 // (in 1/256); the stage-1 waves take the rest after their stage-1 unit.
 constexpr int kFusedSplit = 208;
@@ -141,7 +126,7 @@ struct SfxLds {
     static constexpr int kTab = kWtot + 64;               // int pair tab[kTable + 8] (8 padding entries)
     static constexpr int kPw = kTab + (kTable + 8) * 8;  // float pw[NW][8][8] p rows (dims-major)
     static constexpr int kQs = kPw + NW * 8 * 8 * 4;                     // bf16 q[kQSlots][G][kD]
-    static constexpr int kX = G <= 4 ? 2 : 1;                            // exchange ring slots
+    static constexpr int kX = TOK || G <= 4 ? 2 : 1;                     // exchange ring slots
     static constexpr int kXo = kQs + kQSlots * G * kD * 2;               // float xo[kX][NW][G][kD]
     static constexpr int kXml = kXo + kX * NW * G * kD * 4;              // float xml[kX][NW][G][2]
     static constexpr int kXsync = kXml + kX * NW * G * 2 * 4;            // int cnt[kX], gen[kX]
@@ -155,7 +140,6 @@ struct SfxLds {
                       kSo % 16 == 0,
                   "aligned LDS rows");
 };
-static_assert(SfxLds<kMaxGroup, kWaves>::kBytes <= 80 * 1024, "two stand-alone workgroups per CU");
 
 // window table entry: [0] = page id (-1: not a valid page), [1] = packed fields
 __device__ __forceinline__ int tab_tv(int y) { return y & 127; }  // valid tokens 1 .. 64
@@ -307,10 +291,11 @@ __device__ __forceinline__ int64_t clamp_len(const SuffixArgs &a, int64_t kvl) {
 // barrier. Windows hold 8 NW tokens.
 //
 // Two bodies:
-// * TOK = false (dims-major, vector ALU): lane (hf, dd) holds dims 4dd .. 4dd+3
-//   of 4 tokens; p reaches it through a per-wave LDS row and q is read from LDS
-//   per window. 4 accumulators per head: fits 128 registers.
-// * TOK = true (token-major on the matrix cores, G <= 4, 4 waves): a wave owns 8
+// * TOK = false (dims-major, vector ALU; the fused kernel above 4 heads): lane
+//   (t, c) holds token t and dims 8c .. 8c+7 and 64+8c .. 64+8c+7 of K; lane
+//   (hf, dd) holds dims 4dd .. 4dd+3 of 4 tokens of V, p reaches it through a
+//   per-wave LDS row and q is read from LDS per window. 4 accumulators per head.
+// * TOK = true (token-major on the matrix cores, 4 waves): a wave owns 8
 //   tokens of every window, and lane (g, n) = (lane / 16, lane % 16):
 // * S^T = K q^T on v_mfma_f32_16x16x32_bf16: A = K, row n = token n of the wave's
 //   8 (rows 8-15 read nothing: zeros), dims 32 s + 8 g .. + 7 at step s, straight
@@ -340,7 +325,7 @@ template <int G, int NW, int D, bool TOK, class Bar>
 __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS char *smem, int lb, int tid,
                                                    const Bar &bar, CK_LDS int *scan_flag = nullptr,
                                                    const CK_LDS char *scan_src = nullptr) {
-    static_assert(!TOK || (G <= 4 && NW == 4), "token-major body: at most 4 query heads per group, 4 waves");
+    static_assert(!TOK || NW == 4, "token-major body: 4 waves");
     static_assert(D + 1 <= 8, "table padding: D + 1 entries past a phase");
     constexpr int NB = D + 1;  // register ring slots: D windows in flight + the one in use
     constexpr int kThr = NW * 64;
@@ -486,11 +471,6 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     u32x4 kbuf[NB][TOK ? 4 : 2];
     using VSlot = std::conditional_t<TOK, u32x4[2], u32x2[4]>;
     VSlot vbuf[NB];
-    // dims-major: q in registers from the window that opens a segment in the
-    // stand-alone body above 4 heads (one workgroup per CU, so the 8 G registers
-    // cost no occupancy); else q is read from LDS per window
-    constexpr bool kQReg = G > 4 && NW == kWaves;
-    u32x4 qr[kQReg ? G : 1][2];  // this lane's 16 q dims of each head
     int eyr[NB];               // packed table fields of the window in each ring slot
     constexpr int kPwRow = (G + 3) / 4 * 4;  // floats per token in this wave's p rows
     static_assert(kPwRow <= 8, "p row");
@@ -746,10 +726,6 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                 l[h] = 0.f;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[h][e] = 0.f;
-                if constexpr (kQReg) {
-                    qr[h][0] = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2));
-                    qr[h][1] = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2) + 128);
-                }
             }
         }
         if (t1 > 0) {
@@ -757,14 +733,10 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             float s[G];  // scores, then p in place
             bool trig = false;
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
-                if constexpr (kQReg) {
-                    s[h] = sum8(dot16(k0, k1, qr[h][0], qr[h][1])) * a.scale_log2;
-                } else {
-                    const u32x4 q0 = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2));
-                    const u32x4 q1 = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2) + 128);
-                    s[h] = sum8(dot16(k0, k1, q0, q1)) * a.scale_log2;
-                }
+            for (int h = 0; h < G; ++h) {  // q from LDS per window
+                const u32x4 q0 = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2));
+                const u32x4 q1 = *reinterpret_cast<const CK_LDS u32x4 *>(qrow + h * (kD * 2) + 128);
+                s[h] = sum8(dot16(k0, k1, q0, q1)) * a.scale_log2;
             }
             if (t1 < 8) {
 #pragma unroll
@@ -1067,23 +1039,18 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
     }
 }
 
-// Up to 4 query heads per group: the token-major body on the matrix cores (the
-// fused kernel's streaming body) on 4 waves, two workgroups per CU (64 KB of LDS
-// and at most 256 registers each).
+// The stand-alone stream kernel: the token-major body on the matrix cores (the
+// fused kernel's streaming body) on 4 waves and at most 256 registers; two
+// workgroups per CU up to 4 query heads per group (64 KB of LDS each), one above
+// (103 KB at 8 heads: the grid's second half runs as the first half's
+// workgroups finish; a 4-segment layout that fits two per CU measured no faster).
 template <int G>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void suffix_stream_kernel(SuffixArgs a) {
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-    suffix_stream_body<G, 4, kFusedTokDepth, true>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
+    suffix_stream_body<G, 4, kTokDepth, true>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
 }
-static_assert(SfxLds<4, 4, true>::kBytes <= 80 * 1024, "two token-major stream workgroups per CU");
-// Above 4 query heads per group: the dims-major body on 8 waves; its per-head
-// state needs more registers, and the grid's second half runs as the first
-// half's workgroups finish.
-template <int G>
-__global__ __launch_bounds__(kThreads) void suffix_stream_wide_kernel(SuffixArgs a) {
-    extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-    suffix_stream_body<G, kWaves, kDepth, false>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
-}
+static_assert(SfxLds<4, 4, true>::kBytes <= 80 * 1024, "two stand-alone workgroups per CU up to 4 heads");
+static_assert(SfxLds<kMaxGroup, 4, true>::kBytes <= 160 * 1024, "one above");
 
 // Folds the partials of one query head of a sequence cut by chunk boundaries
 // (chunks ca < cb): the tail slot (1) of chunk ca and the head slot (0) of every
@@ -1367,7 +1334,7 @@ __global__ __launch_bounds__(512) void cascade_fused_kernel(s1::Stage1Args s1a, 
         constexpr int kRoleRot = 3;
         const int g = ((int)blockIdx.x + kRoleRot) % sa.kv_heads, j = (int)blockIdx.x / sa.kv_heads;
         // the streaming waves scan the lengths; the stage-1 waves reuse that scan
-        suffix_stream_body<G, 4, (G <= 4 ? kFusedTokDepth : kFusedDepth), (G <= 4)>(
+        suffix_stream_body<G, 4, (G <= 4 ? kTokDepth : kFusedDepth), (G <= 4)>(
             sa, smem + (role ? 0 : kFusedS1Lds), (2 * j + role) * sa.kv_heads + g, threadIdx.x & 255, bar, bars + 4,
             role ? smem + kFusedS1Lds : nullptr);
     }
@@ -1398,17 +1365,10 @@ int launch_fused(const s1::Stage1Args &s1a, int64_t n1, const SuffixArgs &a, con
 template <int G>
 int launch_suffix(const SuffixArgs &a, bool fixup, const EpilogueArgs *epi, hipStream_t st) {
     static std::atomic<uint64_t> lds_set{0};
-    constexpr int kLds = G <= 4 ? SfxLds<G, 4, true>::kBytes : SfxLds<G, kWaves>::kBytes;
-    const void *fn;
-    if constexpr (G <= 4) fn = reinterpret_cast<const void *>(&suffix_stream_kernel<G>);
-    else fn = reinterpret_cast<const void *>(&suffix_stream_wide_kernel<G>);
-    int rc = ensure_dynamic_lds(fn, kLds, lds_set);
+    constexpr int kLds = SfxLds<G, 4, true>::kBytes;
+    int rc = ensure_dynamic_lds(reinterpret_cast<const void *>(&suffix_stream_kernel<G>), kLds, lds_set);
     if (rc != CK_OK) return rc;
-    if constexpr (G <= 4)
-        hipLaunchKernelGGL(suffix_stream_kernel<G>, dim3((unsigned)(a.kv_heads * a.chunks)), dim3(256), kLds, st, a);
-    else
-        hipLaunchKernelGGL(suffix_stream_wide_kernel<G>, dim3((unsigned)(a.kv_heads * a.chunks)), dim3(kThreads),
-                           kLds, st, a);
+    hipLaunchKernelGGL(suffix_stream_kernel<G>, dim3((unsigned)(a.kv_heads * a.chunks)), dim3(256), kLds, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
     if (fixup)
