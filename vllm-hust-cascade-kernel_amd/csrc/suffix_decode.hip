@@ -521,11 +521,11 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             kf[s4] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(kfoff + 64 * s4), 0, 0));
     };
 
-    // Token-major windows issue their K and V halves at different points of a step
-    // (K before the scores, V after the values of the window whose slot it reuses).
-    auto issue_half = [&](const char *base, const TokWin &w, u32x4 &x0, u32x4 &x1) __attribute__((always_inline)) {
+    // token-major: a window's V rows (lane (t, c): token t, bytes 16 c and 128 + 16 c),
+    // issued after the values of the window whose ring slot they reuse
+    auto issue_v = [&](const TokWin &w, u32x4 &x0, u32x4 &x1) __attribute__((always_inline)) {
         const __amdgpu_buffer_rsrc_t r =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base + w.off), (short)0, w.range, kRsrcFlags);
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(vbase + w.off), (short)0, w.range, kRsrcFlags);
         x0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)koff, 0, 0));
         x1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(koff + 128), 0, 0));
     };
@@ -851,7 +851,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
             sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kbuf[J][s4]),
                                                          __builtin_bit_cast(bf16x8, qf[s4]), sc, 0, 0, 0);
         pv_tok(vbuf[JI]);
-        issue_half(vbase, wi, vbuf[JI][0], vbuf[JI][1]);
+        issue_v(wi, vbuf[JI][0], vbuf[JI][1]);
         if (tab_last(eyp)) close_seg(tab_b(eyp));
         eypend = ey;
         float s[4];  // scores of tokens 4 mg + r, head mn; then p
@@ -986,7 +986,7 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
                 const i32x2 e = tab[j];  // j < D: a padding entry when j >= np
                 const TokWin w = tok_win(e);
                 issue_kfrag(w, kbuf[j]);
-                issue_half(vbase, w, vbuf[j][0], vbuf[j][1]);
+                issue_v(w, vbuf[j][0], vbuf[j][1]);
                 eyr[j] = __builtin_amdgcn_readfirstlane(e[1]);
             } else {
                 const i32x2 e = tab[j];  // j < D: a padding entry when j >= np
