@@ -64,6 +64,10 @@ SUFFIX_CASES = [
     ("gqa16_h64_kvh4", 5, [700, 0, 1025, 64, 3000], 64, 4),
     ("gqa12_h48_kvh4", 3, [129, 2000, 1], 48, 4),
     ("gqa11_h11_kvh1", 3, [500, 77, 1300], 11, 1),
+    # odd group sizes: the matrix-core body's padding heads (columns G .. 15)
+    ("gqa3_h12_kvh4", 5, [1, 300, 65, 0, 1500], 12, 4),
+    ("gqa5_h20_kvh4", 4, [129, 2000, 7, 640], 20, 4),
+    ("gqa7_h28_kvh4", 3, [900, 33, 257], 28, 4),
 ]
 
 
@@ -133,9 +137,13 @@ CASCADE_CFGS = [
     (40, 16, 2, 0, "no_prefix"),     # empty prefix: the suffix alone
     (3, 8, 8, 256, "all_empty"),     # every suffix empty: the prefix alone
     (6, 64, 4, 640, "long_cut"),     # 16 query heads per kv head: two kv head groups
+    (10, 6, 2, 512, "geo512"),       # G = 3, 2 and 1 with suffixes: the fused matrix-core body's padding heads
+    (4, 4, 2, 384, "with_empty"),
+    (9, 8, 8, 256, "geo512"),
+    (8, 14, 2, 512, "geo512"),       # G = 7: the fused kernel's dims-major streaming waves
 ]
 CASCADE_IDS = ["config1_b8_h8", "b16_h32_geo", "empty_suffix", "gqa8_long_cut", "empty_prefix", "all_suffix_empty",
-               "gqa16_long_cut"]
+               "gqa16_long_cut", "gqa3_geo", "gqa2_with_empty", "mha_geo", "gqa7_geo"]
 # the three-op composition cannot take an empty prefix: fa_fp32_stage1 requires kv
 # seqlens >= 1 (the reference's op_host contract), so that case runs fused only
 CASCADE_RUNS = [(cfg, fused) for cfg in CASCADE_CFGS for fused in (True, False) if fused or cfg[3] > 0]
