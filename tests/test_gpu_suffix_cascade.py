@@ -90,6 +90,35 @@ def test_suffix_geometric_lengths():
     _check_suffix(inp, out, lse, H)
 
 
+def _stand_alone_chunk_segments(kvs, num_heads, kv_heads):
+    """Most sequences any chunk of the stand-alone suffix grid holds (host
+    restatement: 32-token windows, 512 / kv head groups equal chunks)."""
+    groups = kv_heads * ((num_heads // kv_heads + 7) // 8)
+    P = max(512 // groups, 1)
+    wins = [(int(x) + 31) // 32 for x in kvs]
+    cw = np.concatenate([[0], np.cumsum(wins)])
+    W = int(cw[-1])
+    most = 0
+    for c in range(P):
+        c0, c1 = c * W // P, (c + 1) * W // P
+        most = max(most, sum(1 for b in range(len(kvs)) if cw[b + 1] > cw[b] and cw[b] < c1 and cw[b + 1] > c0))
+    return most
+
+
+@pytest.mark.parametrize("B,H,KVH,seed", [(768, 32, 8, 11), (640, 64, 8, 12)], ids=["g4_b768", "g8_b640"])
+def test_suffix_chunks_spanning_table_phases(B, H, KVH, seed):
+    """Hundreds of short suffixes (1-20 tokens, some empty): stand-alone chunks hold
+    more than the 8 sequences of one table phase, so the matrix-core stream body
+    crosses phase boundaries at 4 and at 8 query heads per group."""
+    rng = np.random.default_rng(seed)
+    kvs = rng.integers(1, 21, size=B)
+    kvs[rng.random(B) < 0.1] = 0
+    assert _stand_alone_chunk_segments(kvs, H, KVH) > 8  # the premise: chunks span phases
+    inp = paged_inputs(B, kvs, H, KVH, seed=seed, permute=True)
+    out, lse = _suffix(inp)
+    _check_suffix(inp, out, lse, H)
+
+
 def test_suffix_abi_matches_torch_op():
     from cascade_amd import abi
     inp = paged_inputs(4, [1500, 10, 0, 900], 32, 8, seed=3, permute=True)
