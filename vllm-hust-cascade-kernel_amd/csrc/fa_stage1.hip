@@ -80,26 +80,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
 }
 
 // N-way LSE merge of split partials: 32 threads per row, 4 dims each. One
-// pass with an online maximum; the partials of 8 splits are fetched with
-// independent loads per round so the round trips overlap.
+// pass with an online maximum, 8 splits per rescale step; the first 16 splits'
+// partials are fetched together (one memory round trip at the usual split
+// counts), later ones 8 at a time.
 __global__ __launch_bounds__(256) void stage1_combine_kernel(const float *part_o, const float *part_lse,
                                                              int num_splits, int64_t rows,
                                                              float *out, float *lse) {
-    constexpr int kBatch = 8;
+    constexpr int kBatch = 8;   // splits folded per rescale step
+    constexpr int kPreS = 16;   // splits loaded up front: one memory round trip up to 16 splits
     const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
     const int d4 = threadIdx.x & 31;
     if (row >= rows) return;
     float m = -INFINITY, wsum = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = 0; s0 < num_splits; s0 += kBatch) {
-        float ls[kBatch];
-        float4 o[kBatch];
+    // split s0 + j of a batch: its LSE (-inf past the last split) and O (a clamped,
+    // in-bounds index whose weight is 0)
+    auto load = [&](int s0, float *ls, float4 *o) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
             const int s = s0 + j < num_splits ? s0 + j : num_splits - 1;
             ls[j] = s0 + j < num_splits ? part_lse[(int64_t)s * rows + row] : -INFINITY;
             o[j] = *reinterpret_cast<const float4 *>(part_o + ((int64_t)s * rows + row) * kD + 4 * d4);
         }
+    };
+    auto fold = [&](const float *ls, const float4 *o) __attribute__((always_inline)) {
         float mb = m;
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) mb = fmaxf(mb, ls[j]);
@@ -117,6 +121,21 @@ __global__ __launch_bounds__(256) void stage1_combine_kernel(const float *part_o
             wsum += wgt;
         }
         m = mb;
+    };
+    {
+        float ls[kPreS];
+        float4 o[kPreS];
+#pragma unroll
+        for (int s0 = 0; s0 < kPreS; s0 += kBatch) load(s0, ls + s0, o + s0);
+#pragma unroll
+        for (int s0 = 0; s0 < kPreS; s0 += kBatch)
+            if (s0 < num_splits) fold(ls + s0, o + s0);
+    }
+    for (int s0 = kPreS; s0 < num_splits; s0 += kBatch) {
+        float ls[kBatch];
+        float4 o[kBatch];
+        load(s0, ls, o);
+        fold(ls, o);
     }
     const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
     *reinterpret_cast<float4 *>(out + row * kD + 4 * d4) =
