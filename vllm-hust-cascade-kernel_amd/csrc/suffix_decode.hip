@@ -103,8 +103,9 @@ constexpr uint32_t kOob = 0x80000000u;  // a buffer offset past every window's r
 constexpr int kRsrcFlags = 0x00020000;  // buffer descriptor word 3 for gfx9 raw loads
 
 // windows of loads in flight per streaming wave: token-major, 2 (24 registers
-// per window and lane; 3 and 4 measured slower in the fused kernel); dims-major
-// (the fused kernel above 4 heads), 4.
+// per window and lane; 3 and 4 measured slower in the fused kernel), 1 in the
+// stand-alone kernel above 4 heads (one workgroup per CU there: 1 measured
+// faster than 2 and 3); dims-major (the fused kernel above 4 heads), 4.
 constexpr int kTokDepth = 2;
 constexpr int kFusedDepth = 4;
 // Share of each fused workgroup's suffix windows that its streaming waves take
@@ -1047,7 +1048,8 @@ __device__ __forceinline__ void suffix_stream_body(const SuffixArgs &a, CK_LDS c
 template <int G>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void suffix_stream_kernel(SuffixArgs a) {
     extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-    suffix_stream_body<G, 4, kTokDepth, true>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x, WgBarrier{});
+    suffix_stream_body<G, 4, (G > 4 ? 1 : kTokDepth), true>(a, (CK_LDS char *)smem_raw, blockIdx.x, threadIdx.x,
+                                                           WgBarrier{});
 }
 static_assert(SfxLds<4, 4, true>::kBytes <= 80 * 1024, "two stand-alone workgroups per CU up to 4 heads");
 static_assert(SfxLds<kMaxGroup, 4, true>::kBytes <= 160 * 1024, "one above");
