@@ -51,9 +51,11 @@ def run(cmd, cwd=None):
 # to AGPRs): the softmax reads and rescales them with VALU instructions every
 # 128 tokens, and AGPR-resident accumulators cost a copy in and out each time.
 # suffix_decode.hip holds the fused cascade kernel, whose stage-1 waves run the
-# same body.
+# same body. Its cascade epilogue takes the arguments of its first loads as
+# leading scalar parameters, which kernarg preloading puts in SGPRs at wave
+# launch (kernels whose first parameter is a struct are left as they are).
 SOURCE_FLAGS = {"fa_stage1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-                "suffix_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+                "suffix_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
 def compile_hip(src):

@@ -67,7 +67,7 @@ struct CascadeLayout {
 
 int cascade_layout(int64_t batch, int64_t num_heads, int64_t kv_heads, int64_t head_dim, int64_t prefix_cap,
                    int64_t suffix_cap, CascadeLayout *L) {
-    if (batch < 0 || prefix_cap < 0 || suffix_cap < 0) return CK_E_INVALID_ARG;
+    if (batch < 0 || batch > 0x7FFFFFFF || prefix_cap < 0 || suffix_cap < 0) return CK_E_INVALID_ARG;
     if (head_dim != kD) return CK_E_UNSUPPORTED;
     if (kv_heads <= 0 || num_heads <= 0 || num_heads % kv_heads != 0) return CK_E_INVALID_ARG;
     if (num_heads > (1 << 16)) return CK_E_INVALID_ARG;

@@ -1155,6 +1155,10 @@ __global__ __launch_bounds__(kMaxGroup * 32) void suffix_fixup_kernel(SuffixArgs
 // Latency, not bytes, bounds it, so the loads go out in dependency order: the
 // window prefix sums, then every stage-1 partial of the row (up to kPreS
 // splits), then the suffix result those sums locate; the arithmetic waits once.
+// What those first loads need (the prefix sums, the stage-1 result and the row
+// arithmetic) comes as scalar kernel parameters ahead of the struct: the
+// compiler preloads leading scalar parameters into SGPRs at wave launch, which
+// takes the kernel-argument load off the first round trip.
 struct EpilogueArgs {
     Stage1Result s1;
     const uint16_t *o2;     // bf16 [nb][H][kD] whole-sequence suffix results
@@ -1173,31 +1177,32 @@ struct EpilogueArgs {
 };
 
 template <int G>
-__global__ __launch_bounds__(kMaxGroup * 32) void cascade_epilogue_kernel(EpilogueArgs e) {
+__global__ __launch_bounds__(kMaxGroup * 32) void cascade_epilogue_kernel(const int32_t *cw, const float *s1o, const float *s1lse,
+                                                                         int64_t rows, int kv_heads, int nb, int num_heads,
+                                                                         int b0, int splits, EpilogueArgs e) {
     constexpr int kBatch = 8;   // splits folded per rescale step
     constexpr int kPreS = 16;   // splits loaded up front
-    const int bl = blockIdx.x / e.kv_heads;
-    const int g = blockIdx.x % e.kv_heads;
+    const int bl = blockIdx.x / kv_heads;
+    const int g = blockIdx.x % kv_heads;
     const int hq = threadIdx.x >> 5;
     const int d4 = threadIdx.x & 31;
     const int h = g * G + hq;
-    const int64_t row = (e.b0 + bl) * e.num_heads + h;
-    const int splits = e.s1.splits;
+    const int64_t row = (int64_t)(b0 + bl) * num_heads + h;
 
-    const int64_t beg = e.cw[bl], end = e.cw[bl + 1], W = e.cw[e.nb];
+    const int64_t beg = cw[bl], end = cw[bl + 1], W = cw[nb];
 
     // ---- stage-1 loads: the first kPreS splits of this query row ------------------
     float ls[kPreS];
     float4 os[kPreS];
     if (splits <= 1) {
-        os[0] = *reinterpret_cast<const float4 *>(e.s1.o + row * kD + 4 * d4);
-        ls[0] = e.s1.lse[row * 8];
+        os[0] = *reinterpret_cast<const float4 *>(s1o + row * kD + 4 * d4);
+        ls[0] = s1lse[row * 8];
     } else {
 #pragma unroll
         for (int j = 0; j < kPreS; ++j) {
             const int s = j < splits ? j : splits - 1;
-            ls[j] = e.s1.lse[(int64_t)s * e.s1.rows + row];
-            os[j] = *reinterpret_cast<const float4 *>(e.s1.o + ((int64_t)s * e.s1.rows + row) * kD + 4 * d4);
+            ls[j] = s1lse[(int64_t)s * rows + row];
+            os[j] = *reinterpret_cast<const float4 *>(s1o + ((int64_t)s * rows + row) * kD + 4 * d4);
         }
     }
 
@@ -1209,7 +1214,7 @@ __global__ __launch_bounds__(kMaxGroup * 32) void cascade_epilogue_kernel(Epilog
         const int ca = cm.owner(beg);
         const int cb = cm.owner(end - 1);
         if (ca == cb) {
-            const int64_t r2 = (int64_t)bl * e.num_heads + h;
+            const int64_t r2 = (int64_t)bl * num_heads + h;
             const uint2 w = *reinterpret_cast<const uint2 *>(e.o2 + r2 * kD + 4 * d4);
             o2 = make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
             l2 = e.lse2[r2];
@@ -1256,8 +1261,8 @@ __global__ __launch_bounds__(kMaxGroup * 32) void cascade_epilogue_kernel(Epilog
 #pragma unroll
             for (int j = 0; j < kBatch; ++j) {
                 const int s = s0 + j < splits ? s0 + j : splits - 1;
-                lb[j] = e.s1.lse[(int64_t)s * e.s1.rows + row];
-                ob[j] = *reinterpret_cast<const float4 *>(e.s1.o + ((int64_t)s * e.s1.rows + row) * kD + 4 * d4);
+                lb[j] = s1lse[(int64_t)s * rows + row];
+                ob[j] = *reinterpret_cast<const float4 *>(s1o + ((int64_t)s * rows + row) * kD + 4 * d4);
             }
             step(lb, ob, s0);
         }
@@ -1349,6 +1354,12 @@ int64_t ceil_div(int64_t x, int64_t y) { return (x + y - 1) / y; }
 int64_t group_parts(int64_t num_heads, int64_t chunks) { return num_heads * chunks * 2; }
 
 template <int G>
+void launch_epilogue(const EpilogueArgs &e, unsigned grid, hipStream_t st) {
+    hipLaunchKernelGGL(cascade_epilogue_kernel<G>, dim3(grid), dim3(32 * G), 0, st, e.cw, e.s1.o, e.s1.lse, e.s1.rows,
+                       e.kv_heads, e.nb, e.num_heads, (int)e.b0, e.s1.splits, e);
+}
+
+template <int G>
 int launch_fused(const s1::Stage1Args &s1a, int64_t n1, const SuffixArgs &a, const EpilogueArgs &epi,
                  hipStream_t st) {
     static std::atomic<uint64_t> lds_set{0};
@@ -1360,7 +1371,7 @@ int launch_fused(const s1::Stage1Args &s1a, int64_t n1, const SuffixArgs &a, con
     hipLaunchKernelGGL(cascade_fused_kernel<G>, dim3((unsigned)grid), dim3(512), kLds, st, s1a, (int)n1, a, (int)n2);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
-    hipLaunchKernelGGL(cascade_epilogue_kernel<G>, dim3((unsigned)(a.batch * a.kv_heads)), dim3(32 * G), 0, st, epi);
+    launch_epilogue<G>(epi, (unsigned)(a.batch * a.kv_heads), st);
     CK_RETURN_LAUNCH();
 }
 
@@ -1375,14 +1386,12 @@ int launch_suffix(const SuffixArgs &a, bool fixup, const EpilogueArgs *epi, hipS
     if (e != hipSuccess) return static_cast<int>(e);
     if (fixup)
         hipLaunchKernelGGL(suffix_fixup_kernel<G>, dim3((unsigned)(a.batch * a.kv_heads)), dim3(32 * G), 0, st, a);
-    if (epi)
-        hipLaunchKernelGGL(cascade_epilogue_kernel<G>, dim3((unsigned)(a.batch * a.kv_heads)), dim3(32 * G), 0, st,
-                           *epi);
+    if (epi) launch_epilogue<G>(*epi, (unsigned)(a.batch * a.kv_heads), st);
     CK_RETURN_LAUNCH();
 }
 
 int check_suffix_dims(int64_t batch, int64_t num_heads, int64_t kv_heads, int64_t head_dim, int64_t kv_cap) {
-    if (batch < 0 || kv_cap < 0) return CK_E_INVALID_ARG;
+    if (batch < 0 || batch > 0x7FFFFFFF || kv_cap < 0) return CK_E_INVALID_ARG;  // sequence indices are 32-bit
     if (head_dim != kD) return CK_E_UNSUPPORTED;
     if (kv_heads <= 0 || num_heads <= 0 || num_heads % kv_heads != 0) return CK_E_INVALID_ARG;
     if (num_heads > (1 << 16)) return CK_E_INVALID_ARG;
