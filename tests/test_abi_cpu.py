@@ -140,6 +140,9 @@ def test_cascade_plan_and_validation():
     assert L.ck_cascade_decode_plan(4, 32, 8, 64, 128, 128, ctypes.byref(out)) == -4    # D != 128
     assert L.ck_cascade_decode_plan(4, 30, 8, 128, 128, 128, ctypes.byref(out)) == -1   # H % KVH
     assert L.ck_cascade_decode_plan(4, 32, 8, 128, 128, 128, None) == -2
+    # sequence indices are 32-bit: a batch of 2^31 sequences is refused by both plans
+    assert L.ck_cascade_decode_plan(1 << 31, 32, 8, 128, 128, 128, ctypes.byref(out)) == -1
+    assert L.ck_suffix_decode_plan(1 << 31, 32, 8, 128, 128, ctypes.byref(out), ctypes.byref(out)) == -1
     p = ctypes.c_void_p(16)  # never dereferenced: every call below fails validation first
 
     def call(batch=4, block=128, pcols=1, pcap=128, scols=1, scap=128, ws=None, wsb=0, q=p, layout=0):
