@@ -1159,6 +1159,8 @@ __global__ __launch_bounds__(kMaxGroup * 32) void suffix_fixup_kernel(SuffixArgs
 // arithmetic) comes as scalar kernel parameters ahead of the struct: the
 // compiler preloads leading scalar parameters into SGPRs at wave launch, which
 // takes the kernel-argument load off the first round trip.
+// The host fills the whole struct; launch_epilogue passes s1, cw, b0, nb,
+// num_heads and kv_heads again as the leading parameters the kernel reads.
 struct EpilogueArgs {
     Stage1Result s1;
     const uint16_t *o2;     // bf16 [nb][H][kD] whole-sequence suffix results
