@@ -1118,14 +1118,17 @@ __device__ __forceinline__ void fold_cut(const float *part_o, const float *part_
 
 // One workgroup of 32 G threads per (sequence, kv head): empty suffixes get
 // O = 0, LSE = -inf; a sequence cut by chunk boundaries gets its partials
-// folded; others return.
+// folded; others return. The window prefix sums and the grid arithmetic come as
+// leading scalar parameters (preloaded into SGPRs at wave launch, as for the
+// cascade epilogue), so the first load waits for no kernel-argument load.
 template <int G>
-__global__ __launch_bounds__(kMaxGroup * 32) void suffix_fixup_kernel(SuffixArgs a) {
-    const int b = blockIdx.x / a.kv_heads;
-    const int g = blockIdx.x % a.kv_heads;
+__global__ __launch_bounds__(kMaxGroup * 32) void suffix_fixup_kernel(const int32_t *cw, int kv_heads, int batch,
+                                                                      SuffixArgs a) {
+    const int b = blockIdx.x / kv_heads;
+    const int g = blockIdx.x % kv_heads;
     const int hq = threadIdx.x >> 5;
     const int d4 = threadIdx.x & 31;
-    const int64_t beg = a.cw_out[b], end = a.cw_out[b + 1], W = a.cw_out[a.batch];
+    const int64_t beg = cw[b], end = cw[b + 1], W = cw[batch];
     const int64_t row = (int64_t)b * a.num_heads + g * G + hq;
     if (end == beg) {
         *reinterpret_cast<uint2 *>(a.out + row * kD + 4 * d4) = make_uint2(0, 0);
@@ -1387,7 +1390,8 @@ int launch_suffix(const SuffixArgs &a, bool fixup, const EpilogueArgs *epi, hipS
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
     if (fixup)
-        hipLaunchKernelGGL(suffix_fixup_kernel<G>, dim3((unsigned)(a.batch * a.kv_heads)), dim3(32 * G), 0, st, a);
+        hipLaunchKernelGGL(suffix_fixup_kernel<G>, dim3((unsigned)(a.batch * a.kv_heads)), dim3(32 * G), 0, st,
+                           (const int32_t *)a.cw_out, a.kv_heads, a.batch, a);
     if (epi) launch_epilogue<G>(*epi, (unsigned)(a.batch * a.kv_heads), st);
     CK_RETURN_LAUNCH();
 }
