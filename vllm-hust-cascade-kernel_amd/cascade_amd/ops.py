@@ -1,4 +1,5 @@
-"""Python-facing wrappers over ``torch.ops.npu.*`` (names follow the reference).
+"""The cascade compositions over ``torch.ops.npu.*``; the single ops are called as
+``torch.ops.npu.<name>`` directly, as in the reference.
 
 ``cascade_decode`` is the caller-side composition the reference documents
 (ascend-kernel/README.md:160-201) -- stage-1 over the shared prefix in the
@@ -7,38 +8,6 @@ and the LSE merge -- as one fused op; ``cascade_decode_unfused`` composes the
 three separate ops the same way the reference does.
 """
 import torch
-
-
-def fa_fp32_stage1(query, key, value, block_table, actual_q_seqlens, actual_kv_seqlens, q_seqlen_value=0):
-    return torch.ops.npu.fa_fp32_stage1(query, key, value, block_table, actual_q_seqlens,
-                                        actual_kv_seqlens, q_seqlen_value)
-
-
-def lse_merge(o1, o2, lse1, lse2, out_code=0):
-    return torch.ops.npu.lse_merge(o1, o2, lse1, lse2, out_code)
-
-
-def lse_merge_with_lse(o1, o2, lse1, lse2, out_code=0):
-    return torch.ops.npu.lse_merge_with_lse(o1, o2, lse1, lse2, out_code)
-
-
-def suffix_decode(query, key, value, block_table, actual_kv_seqlens, kv_layout=0):
-    """kv_layout 0: key/value [numBlocks, 128, KVH, D] (NHD); 1: [numBlocks, KVH, 128, D] (BNSD)."""
-    return torch.ops.npu.suffix_decode(query, key, value, block_table, actual_kv_seqlens, kv_layout)
-
-
-def f3_gateup_epilogue(a, b, workspace=None, out_d=None, mode=1):
-    return torch.ops.npu.f3_gateup_epilogue(a, b, workspace, out_d, mode)
-
-
-def add_rms_norm_stats(x1, x2, gamma=None, beta=None, eps=1e-6, mode=0):
-    """Residual add + RMSNorm statistics (+ apply); see include/cascade_kernels.h."""
-    return torch.ops.npu.add_rms_norm_stats(x1, x2, gamma, beta, eps, mode)
-
-
-def swiglu_gate_up(a, b):
-    """D = silu(a @ b[:I].T) * (a @ b[I:].T) in one fused GEMM (mode 1)."""
-    return torch.ops.npu.f3_gateup_epilogue(a, b, None, None, 1)[0]
 
 
 def cascade_decode(query, prefix_key, prefix_value, prefix_block_table, prefix_kv_seqlens,
